@@ -1,0 +1,319 @@
+#!/usr/bin/env python3
+"""Benchmark of the optimized pre-LN transformer forward on one MI355X.
+
+Metric: p50 forward latency (us) per config, and fp16 MFMA TFLOP/s as a fraction of
+the MI355X dense fp16 peak.  A "step" is one forward call ``opt(x, mask)`` of the headline
+workload (default C5: 12 layers, D1024, H16, F4096, B2, S4096, causal) on resident fp16 inputs.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C5] [--configs all|none|C1,..]
+
+Prints ONE JSON line.  Per the reference harness (benchmarks/torch_transformer_benchmark.py:477-583)
+every call is bracketed by HIP events on the current stream, the optimized and eager-fp16 models
+alternate rounds, p50/p90 use the linearly interpolated percentile (:427-439) and
+tokens/s = B*S / p50.  The K timed steps are also bracketed by a device synchronisation on both
+sides, which gives ``ms_per_step``.  Inside the same run each kernel of one layer is timed in
+isolation (HIP events on the stream it is launched on) to give the roofline of the dominant
+kernel, and the CPU fp32 oracle is timed on a bounded sample on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import copy
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+from tttj_2026_amd import make_optimized_transformer, ops, roofline
+from tttj_2026_amd.configs import WORKLOADS, WORKLOAD_ORDER, build_model, workload_inputs
+
+METRIC = "p50 fwd latency (us) per config; fp16 MFMA TFLOP/s as % of MI355X peak"
+PEAK_TFLOPS = roofline.MI355X_FP16_DENSE_TFLOPS
+PEAK_GBPS = roofline.MI355X_HBM_GBPS
+
+
+def percentile(values, q):
+    v = sorted(values)
+    if len(v) == 1:
+        return v[0]
+    pos = (len(v) - 1) * q
+    lo, hi = math.floor(pos), math.ceil(pos)
+    return v[lo] if lo == hi else v[lo] * (hi - pos) + v[hi] * (pos - lo)
+
+
+def time_calls(fn, iters):
+    """Per-call HIP-event times (ms) of ``fn`` on the current stream."""
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    torch.cuda.synchronize()
+    for i in range(iters):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in zip(starts, ends)]
+
+
+def lengths_of(mask, cfg):
+    if mask is None:
+        return None
+    return [int(v) for v in mask.sum(dim=1).tolist()]
+
+
+def bench_workload(name, steps, warmup, rounds, eager, dev):
+    w = WORKLOADS[name]
+    cfg = w.config
+    model = build_model(cfg).half().to(dev).eval()
+    opt = make_optimized_transformer(copy.deepcopy(model))
+    x16, mask = workload_inputs(name)
+    xd = x16.to(dev)
+    md = None if mask is None else mask.to(dev)
+    with torch.inference_mode():
+        for _ in range(warmup):
+            opt(xd, md)
+        if eager:
+            for _ in range(max(2, warmup // 4)):
+                model(xd, md)
+        torch.cuda.synchronize()
+        opt_s, eager_s = [], []
+        per = max(1, steps // rounds)
+        for r in range(rounds):
+            order = (0, 1) if r % 2 == 0 else (1, 0)
+            for which in order:
+                if which == 0:
+                    opt_s += time_calls(lambda: opt(xd, md), per)
+                elif eager:
+                    eager_s += time_calls(lambda: model(xd, md), max(1, per // 2))
+    p50 = statistics.median(opt_s)
+    lens = lengths_of(mask, cfg)
+    useful = roofline.forward_flops(cfg, lens)
+    dense = roofline.forward_flops(cfg)
+    out = {
+        "p50_us": p50 * 1e3,
+        "p90_us": percentile(opt_s, 0.9) * 1e3,
+        "tokens_per_s": cfg.batch_size * cfg.seq_len / (p50 * 1e-3),
+        "useful_gflop": useful / 1e9,
+        "dense_gflop": dense / 1e9,
+        "useful_tflops": useful / (p50 * 1e-3) / 1e12,
+        "mfma_frac_useful": useful / (p50 * 1e-3) / 1e12 / PEAK_TFLOPS,
+        "samples": len(opt_s),
+    }
+    if eager_s:
+        e50 = statistics.median(eager_s)
+        out.update(eager_p50_us=e50 * 1e3, eager_p90_us=percentile(eager_s, 0.9) * 1e3,
+                   speedup_vs_eager=e50 / p50)
+    return out, (model, opt, xd, md, x16, mask)
+
+
+def kernel_breakdown(name, dev, iters=20):
+    """Time each kernel of one layer in isolation (HIP events on the launch stream)."""
+    cfg = WORKLOADS[name].config
+    B, S, D, H, F = cfg.batch_size, cfg.seq_len, cfg.d_model, cfg.num_heads, cfg.ffn_dim
+    T, hd = B * S, D // H
+    x16, mask = workload_inputs(name)
+    g = torch.Generator().manual_seed(5)
+    rnd = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).half().to(dev)
+    x = x16.to(dev).reshape(T, D)
+    md = None if mask is None else mask.to(dev)
+    lnw, lnb = rnd(D, sc=0.1) + 1, rnd(D, sc=0.1)
+    wqkv, bqkv = rnd(3 * D, D, sc=D ** -0.5), rnd(3 * D, sc=0.1)
+    wo, bo = rnd(D, D, sc=D ** -0.5), rnd(D, sc=0.1)
+    w1, b1 = rnd(F, D, sc=D ** -0.5), rnd(F, sc=0.1)
+    w2, b2 = rnd(D, F, sc=F ** -0.5), rnd(D, sc=0.1)
+    xn = ops.layernorm(x, lnw, lnb)
+    q, k, vt = ops.qkv_projection(xn.reshape(B, S, D), wqkv, bqkv, H)
+    ctx = ops.attention(q, k, vt, md, cfg.causal).reshape(T, D)
+    hmid = ops.linear(xn, w1, b1, "gelu")
+    resid = x.clone()
+    lens = lengths_of(mask, cfg)
+    lf = roofline.layer_flops(cfg, lens)
+    kernels = {
+        "layernorm": (lambda: ops.layernorm(x, lnw, lnb), 2, "hbm", roofline.layernorm_bytes(T, D)),
+        "gemm_qkv": (lambda: ops.qkv_projection(xn.reshape(B, S, D), wqkv, bqkv, H), 1, "mfma",
+                     2 * T * 3 * D * D),
+        "attention": (lambda: ops.attention(q, k, vt, md, cfg.causal), 1, "mfma", lf["attention"]),
+        "gemm_out": (lambda: ops.linear(ctx, wo, bo, "resid_masked", residual=resid, valid=md,
+                                        out=resid), 1, "mfma", 2 * T * D * D),
+        "gemm_ffn_in": (lambda: ops.linear(xn, w1, b1, "gelu"), 1, "mfma", 2 * T * D * F),
+        "gemm_ffn_out": (lambda: ops.linear(hmid, w2, b2, "masked_resid", residual=resid,
+                                            valid=md, out=resid), 1, "mfma", 2 * T * F * D),
+    }
+    res = {}
+    for kname, (fn, per_layer, bound, work) in kernels.items():
+        for _ in range(3):
+            fn()
+        t = statistics.median(time_calls(fn, iters))
+        # ops wrappers allocate outputs; the allocator is warm, so events see the kernel itself
+        entry = {"avg_ms": t, "per_layer": per_layer, "bound": bound,
+                 "ms_per_forward": t * per_layer * cfg.num_layers}
+        if bound == "mfma":
+            entry["achieved_tflops"] = work / (t * 1e-3) / 1e12
+            entry["frac"] = entry["achieved_tflops"] / PEAK_TFLOPS
+            entry["flops"] = work
+        else:
+            entry["achieved_gbps"] = work / (t * 1e-3) / 1e9
+            entry["frac"] = entry["achieved_gbps"] / PEAK_GBPS
+            entry["bytes"] = work
+        res[kname] = entry
+    return res
+
+
+def cpu_baseline(name, budget_s, gpu_out=None):
+    """Time the fp32 CPU oracle (this repo's restatement of BaselineTransformer) on host cores."""
+    from oracle import transformer_oracle as O
+
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cores = max(1, min(cores, 16))
+    torch.set_num_threads(cores)
+    w = WORKLOADS[name]
+    cfg = w.config
+    model = build_model(cfg)
+    params = O.params_fp32(copy.deepcopy(model).half())
+    x16, mask = workload_inputs(name)
+    x = x16.float()
+    n_layers = cfg.num_layers
+
+    def run(nl):
+        p = {k: v for k, v in params.items()
+             if not k.startswith("layers.") or int(k.split(".")[1]) < nl}
+        t0 = time.perf_counter_ns()
+        y = O.forward(p, x, mask, cfg.num_heads, cfg.causal)
+        return (time.perf_counter_ns() - t0) / 1e6, y
+
+    t1, _ = run(1)  # one layer: warm-up and estimate
+    est_full = t1 * n_layers
+    result = {"unit": "us", "cores": cores, "kind": "port"}
+    if est_full / 1e3 <= budget_s:
+        reps = max(1, min(5, int(budget_s * 1e3 / max(est_full, 1.0))))
+        times, y = [], None
+        for _ in range(reps):
+            t, y = run(n_layers)
+            times.append(t)
+        result["value"] = statistics.median(times) * 1e3
+        result["sample"] = f"{reps} full forward(s) of {name}, median"
+        if gpu_out is not None:
+            d = (gpu_out.float().cpu() - y).abs()
+            result["gpu_vs_oracle"] = {"max_abs": float(d.max()), "mean_abs": float(d.mean())}
+    else:
+        nl = max(1, min(n_layers, int(budget_s * 1e3 / max(t1, 1.0))))
+        t, _ = run(nl)
+        result["value"] = t / nl * n_layers * 1e3
+        result["sample"] = (f"first {nl} of {n_layers} layers of {name} (+final norm), one call, "
+                            f"scaled by {n_layers}/{nl}")
+    torch.set_num_threads(cores)
+    result["torch_threads"] = torch.get_num_threads()
+    try:
+        with open("/proc/cpuinfo") as f:
+            result["cpu_model"] = next(l.split(":", 1)[1].strip() for l in f if "model name" in l)
+    except Exception:
+        pass
+    return result
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="C5", choices=WORKLOAD_ORDER)
+    ap.add_argument("--configs", default="all", help="all | none | comma list of C1..C5")
+    ap.add_argument("--rounds", type=int, default=3)
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU oracle work")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-eager", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the forward shards by sequence with zero collectives; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    name = args.workload
+    cfg = WORKLOADS[name].config
+
+    head, (model, opt, xd, md, x16, mask) = bench_workload(
+        name, args.steps, args.warmup, args.rounds, not args.no_eager, dev)
+    # the K timed steps, bracketed by synchronisation
+    with torch.inference_mode():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            y = opt(xd, md)
+        torch.cuda.synchronize()
+        ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    print(f"[bench] {name} p50 {head['p50_us']:.1f} us", file=sys.stderr, flush=True)
+
+    kernels = kernel_breakdown(name, dev)
+    dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["ms_per_forward"])
+    if dom["bound"] == "mfma":
+        rl = {"kernel": dom_name, "bound": "mfma", "achieved": dom["achieved_tflops"],
+              "peak": PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"], "traffic": None,
+              "work_per_launch": dom["flops"], "avg_launch_ms": dom["avg_ms"]}
+    else:
+        rl = {"kernel": dom_name, "bound": "hbm", "achieved": dom["achieved_gbps"],
+              "peak": PEAK_GBPS, "unit": "GB/s", "frac": dom["frac"], "traffic": None,
+              "work_per_launch": dom["bytes"], "avg_launch_ms": dom["avg_ms"]}
+
+    per_config = {}
+    wanted = [] if args.configs == "none" else (
+        list(WORKLOAD_ORDER) if args.configs == "all" else args.configs.split(","))
+    for other in wanted:
+        if other == name:
+            per_config[other] = head
+            continue
+        per_config[other], _ = bench_workload(other, 100 if other in ("C1", "C2", "C3") else 30,
+                                              20, args.rounds, not args.no_eager, dev)
+        print(f"[bench] {other} p50 {per_config[other]['p50_us']:.1f} us", file=sys.stderr,
+              flush=True)
+    speedups = [v["speedup_vs_eager"] for v in per_config.values() if "speedup_vs_eager" in v]
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(name, args.cpu_budget, gpu_out=y)
+
+    line = {
+        "metric": METRIC,
+        "value": head["p50_us"],
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic: seeded N(0,1) fp16 inputs, seeded default-init weights (no checkpoint)",
+        "config": {"workload": name, "batch": cfg.batch_size, "seq_len": cfg.seq_len,
+                   "d_model": cfg.d_model, "heads": cfg.num_heads, "ffn_dim": cfg.ffn_dim,
+                   "layers": cfg.num_layers, "causal": cfg.causal,
+                   "mask": "right-padded l~U{S/2..S}" if WORKLOADS[name].masked else "none",
+                   "parallelism": "single-gpu"},
+        "p90_us": head["p90_us"],
+        "tokens_per_s": head["tokens_per_s"],
+        "useful_tflops": head["useful_tflops"],
+        "mfma_frac_useful": head["mfma_frac_useful"],
+        "eager_fp16_p50_us": head.get("eager_p50_us"),
+        "speedup_vs_eager": head.get("speedup_vs_eager"),
+        "roofline": rl,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+        "per_config": per_config,
+        "geomean_speedup_vs_eager": (math.exp(sum(map(math.log, speedups)) / len(speedups))
+                                     if speedups else None),
+        "gpu": torch.cuda.get_device_name(dev),
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,126 @@
+/*
+ * tttj_amd.h -- C ABI of the MI355X (gfx950) pre-LN transformer forward library.
+ *
+ * Every entry point takes raw device pointers, plain integer shapes and an explicit HIP stream
+ * (passed as void*, i.e. the value of torch.cuda.current_stream().cuda_stream), returns an int
+ * status (TT_OK = 0) and never throws.  On failure tt_last_error_string() describes the problem.
+ * Activations and weights are IEEE fp16 (passed as void*), masks are one byte per token (a torch
+ * bool tensor's storage: 0 = padded, non-zero = valid).  The library allocates no device memory:
+ * callers pass every buffer, including the workspace.
+ *
+ * The reference exposes this path as Python/Triton functions and one pybind11 extension; each
+ * declaration below names the reference interface it replaces (paths relative to the reference
+ * repository root).
+ */
+#ifndef TTTJ_AMD_H
+#define TTTJ_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define TT_OK 0
+#define TT_ERR_INVALID 1 /* unsupported shape / bad argument, detected before any launch */
+#define TT_ERR_HIP 2     /* a HIP runtime call or kernel launch failed */
+
+/* Epilogues of tt_linear_fwd: Y = X W^T + b, then
+ *   TT_EPI_BIAS           y = acc + b
+ *   TT_EPI_BIAS_GELU      y = gelu_erf(acc + b)
+ *   TT_EPI_RESID_MASKED   y = residual + (valid[row] ? acc + b : 0)      (attention out_proj)
+ *   TT_EPI_MASKED_RESID   y = valid[row] ? residual + acc + b : 0         (ffn_out + block mask)
+ *   TT_EPI_QKV            columns [0,D) -> Q [B,H,S,hd], [D,2D) -> K [B,H,S,hd],
+ *                         [2D,3D) -> V^T [B,H,hd,Sp] with Sp = S rounded up to a multiple of
+ *                         64 (y points at Q; K and V^T follow at offsets B*S*D and 2*B*S*D
+ *                         elements; the V^T region holds B*D*Sp elements).  Needs batch/seq/heads.
+ * `valid` may be NULL (all rows valid).  `residual` may alias `y` (in-place update). */
+#define TT_EPI_BIAS 0
+#define TT_EPI_BIAS_GELU 1
+#define TT_EPI_RESID_MASKED 2
+#define TT_EPI_MASKED_RESID 3
+#define TT_EPI_QKV 4
+
+/* Library version string and the offload architecture it was built for. */
+const char* tt_version(void);
+
+/* Description of the last failure on the calling thread ("" if none). */
+const char* tt_last_error_string(void);
+
+/* Number of visible HIP devices (no kernel launch); <0 on error. */
+int tt_device_count(void);
+
+/* Packed fp16 weight layout.  Replaces the packing of kernels/sequence_resident.py:74-109 and the
+ * offset table of kernels/fused_megakernel.py:28-44 (which assume F == D); generalised to any F.
+ * Per layer, in this order, each segment starting on a 64-element boundary:
+ *   0 norm1.weight[D]  1 norm1.bias[D]  2 Wqkv[3D,D] (q rows, k rows, v rows)  3 bqkv[3D]
+ *   4 out_proj.weight[D,D]  5 out_proj.bias[D]  6 norm2.weight[D]  7 norm2.bias[D]
+ *   8 ffn_in.weight[F,D]  9 ffn_in.bias[F]  10 ffn_out.weight[D,F]  11 ffn_out.bias[D]
+ * then final_norm.weight[D], final_norm.bias[D] after the last layer.
+ * Writes the 12 per-layer segment offsets (elements, relative to the layer start), the layer
+ * stride, the final-norm offset and the total element count. */
+int tt_weight_layout(int d_model, int ffn_dim, int num_layers, int64_t layer_offsets[12],
+                     int64_t* layer_stride, int64_t* final_norm_offset, int64_t* total_elems);
+
+/* Bytes of workspace tt_transformer_fwd needs for this shape. */
+int tt_workspace_bytes(int batch, int seq, int d_model, int num_heads, int ffn_dim,
+                       int64_t* bytes);
+
+/* y[r] = LayerNorm(x[r]) * gamma + beta (eps, biased variance, fp32 statistics), fp16 out;
+ * rows with valid[r] == 0 are written as +0.0 (valid may be NULL).  d % 8 == 0, d <= 8192.
+ * Replaces residual_layer_norm / _residual_layer_norm_kernel (kernels/case8_fusions.py:82-256)
+ * and the standalone LayerNorm of nn.LayerNorm in torch_transformer_benchmark.py:128,130,160. */
+int tt_layernorm_fwd(const void* x, const void* gamma, const void* beta, const uint8_t* valid,
+                     void* y, int rows, int d, float eps, void* stream);
+
+/* Y[M,N] = X[M,K] W[N,K]^T + b with one of the TT_EPI_* epilogues; fp16 in/out, fp32 accumulate
+ * on MFMA.  K % 64 == 0, N % 64 == 0.  For TT_EPI_QKV, N == 3*D with D = heads*head_dim and
+ * M == batch*seq.  Replaces _linear_tile with EPILOGUE 0-3 (kernels/fused_megakernel.py:447-541),
+ * linear_gelu (kernels/case13_linear.py:149-176), the packed-QKV F.linear
+ * (kernels/layerwise_hybrid.py:188-192) and _head_major_qkv_kernel (case13_linear.py:114-146). */
+int tt_linear_fwd(const void* x, const void* w, const void* bias, const void* residual,
+                  const uint8_t* valid, void* y, int m, int n, int k, int epilogue, int batch,
+                  int seq, int heads, void* stream);
+
+/* Test hook: force tile configuration `index` (0: 256x256, 1: 256x128, 2: 128x128, 3: 128x64,
+ * 4: 64x64) for every later GEMM whose N it divides; -1 restores the automatic choice.  Process
+ * wide, not thread-safe.  No counterpart in the reference (its tile choices are compile-time
+ * constants per case, kernels/fused_megakernel.py:121-171). */
+int tt_gemm_tile_override(int index);
+
+/* Per-sequence mask summary used by the attention and GEMM kernels: info[b] = 1 + index of the
+ * last valid token of sequence b (0 if none), info[batch + b] = 1 if the valid tokens of b form a
+ * prefix.  mask may be NULL (then every sequence is a full prefix).  Replaces the host-side
+ * all-valid check of kernels/sequence_resident.py:172-192 without a host synchronisation. */
+int tt_mask_info(const uint8_t* mask, int32_t* info, int batch, int seq, void* stream);
+
+/* Flash attention over the TT_EPI_QKV layout: q, k [B,H,S,hd], vt [B,H,hd,Sp] -> ctx [B,S,H*hd]
+ * token-major.  softmax(q k^T * hd^-0.5) with keys masked when (causal && key > query) or
+ * mask[b,key] == 0; padded query rows are written as +0.0.  hd in {32, 64}.  `info` is the
+ * tt_mask_info output for the same mask (may be NULL only if mask is NULL).  Replaces
+ * _attention_mxhd (kernels/fused_megakernel.py:544-790) and packed_causal_attention
+ * (kernels/case8_attention.py:48-206), and BaselineSelfAttention's score/softmax/PV
+ * (torch_transformer_benchmark.py:97-117). */
+int tt_attention_fwd(const void* q, const void* k, const void* vt, const uint8_t* mask,
+                     const int32_t* info, void* ctx, int batch, int seq, int heads, int head_dim,
+                     int causal, void* stream);
+
+/* Whole forward of the block stack + final norm:
+ *   y = mask(final_norm(block_L(...block_1(x)))), block(x) = mask(x' + W2 gelu(W1 LN2(x') + b1)
+ *   + b2) with x' = x + mask(Wo attn(LN1 x) + bo)
+ * over the packed weights of tt_weight_layout.  x, y [B,S,D] fp16 (y must not alias x), mask
+ * [B,S] bytes or NULL.  `plan` selects the execution strategy: 0 = automatic, 1 = layer-wise
+ * kernels, 2 = persistent whole-model megakernel (only for shapes tt_megakernel_supported
+ * accepts).  Replaces LayerwiseHybridTransformer.forward (kernels/layerwise_hybrid.py:255-361)
+ * and SequenceResidentTransformer.run (kernels/sequence_resident.py:158-225). */
+int tt_transformer_fwd(const void* weights, const void* x, const uint8_t* mask, void* y,
+                       void* workspace, int64_t workspace_bytes, int batch, int seq, int d_model,
+                       int num_heads, int ffn_dim, int num_layers, int causal, int plan,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TTTJ_AMD_H */

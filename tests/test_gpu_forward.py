@@ -1,0 +1,150 @@
+"""End-to-end parity of make_optimized_transformer(model)(x, mask) against the fp32 CPU oracle.
+
+Gate (the acceptance bar): over the whole [B,S,D] fp16 output, max|d| <= 2e-2 and
+mean|d| <= 2e-3 against the oracle run in fp32 on the fp16-rounded weights and inputs, padded rows
+bitwise +0.0, and two consecutive calls bit-identical (the reference's repeat check,
+benchmarks/regression.py:123-134).
+"""
+
+import copy
+
+import pytest
+import torch
+
+from oracle import transformer_oracle as O
+from tttj_2026_amd import PLAN_LAYERWISE, make_optimized_transformer, ops
+from tttj_2026_amd.configs import WORKLOADS, WORKLOAD_ORDER, build_model, make_inputs, workload_inputs
+from tttj_2026_amd.model import TransformerConfig
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(model_cpu, x16, mask, device, perturb_ln=False, **kw):
+    cfg = model_cpu.config
+    if perturb_ln:
+        g = torch.Generator().manual_seed(99)
+        with torch.no_grad():
+            for name, p in model_cpu.named_parameters():
+                if "norm" in name:
+                    p.add_(0.25 * torch.randn(p.shape, generator=g))
+    gpu_model = copy.deepcopy(model_cpu).half().to(device).eval()
+    opt = make_optimized_transformer(copy.deepcopy(gpu_model), **kw)
+    xd = x16.to(device)
+    md = None if mask is None else mask.to(device)
+    with torch.inference_mode():
+        y1 = opt(xd, md).clone()
+        y2 = opt(xd, md)
+    torch.cuda.synchronize()
+    ref = O.forward(O.params_fp32(gpu_model), x16.float(), mask, cfg.num_heads, cfg.causal)
+    res = O.check_tolerance(y1, ref, mask)
+    res["repeat_identical"] = bool(torch.equal(y1, y2))
+    return res, gpu_model, y1, ref
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("name", WORKLOAD_ORDER)
+def test_workload_parity(device, name):
+    w = WORKLOADS[name]
+    model = build_model(w.config)
+    x16, mask = workload_inputs(name)
+    print(f"[parity] {name} {w.description}", flush=True)
+    res, _, _, _ = _run(model, x16, mask, device)
+    print(f"[parity] {name} {res}", flush=True)
+    assert res["passed"], res
+    assert res["repeat_identical"]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("hd", [32, 64])
+def test_nonprefix_mask_and_perturbed_norms(device, causal, hd):
+    cfg = TransformerConfig(3, 96, 256, 256 // hd, 512, 2, causal)
+    model = build_model(cfg, seed=7)
+    x16, _ = make_inputs(cfg, False, 8)
+    g = torch.Generator().manual_seed(9)
+    mask = torch.rand(3, 96, generator=g) > 0.3
+    mask[1] = False          # a fully padded sequence
+    mask[2, :50] = True
+    x16 = x16.masked_fill(~mask[..., None], 0)
+    res, _, _, _ = _run(model, x16, mask, device, perturb_ln=True)
+    assert res["passed"], res
+    assert res["repeat_identical"]
+
+
+@pytest.mark.parametrize("scale", [1e-3, 1.0, 30.0])
+def test_input_scales(device, scale):
+    cfg = TransformerConfig(2, 128, 512, 8, 2048, 2, True)
+    model = build_model(cfg, seed=3)
+    x16, mask = make_inputs(cfg, True, 4)
+    x16 = (x16.float() * scale).half()
+    res, _, _, _ = _run(model, x16, mask, device)
+    assert res["passed"], res
+
+
+def test_runtime_shape_differs_from_config(device):
+    """Any (B, S) works at run time; only d_model/heads/ffn/layers come from the config."""
+    cfg = TransformerConfig(4, 128, 256, 4, 1024, 2, False)
+    model = build_model(cfg, seed=5)
+    run_cfg = TransformerConfig(3, 77, 256, 4, 1024, 2, False)
+    x16, mask = make_inputs(run_cfg, True, 6, min_valid=10)
+    res, _, _, _ = _run(model, x16, mask, device, plan=PLAN_LAYERWISE)
+    assert res["passed"], res
+
+
+def test_eager_fp16_floor_and_no_mask_equivalence(device):
+    name = "C1"
+    w = WORKLOADS[name]
+    model = build_model(w.config)
+    x16, _ = workload_inputs(name)
+    gpu_model = copy.deepcopy(model).half().to(device).eval()
+    opt = make_optimized_transformer(copy.deepcopy(gpu_model))
+    xd = x16.to(device)
+    with torch.inference_mode():
+        eager = gpu_model(xd, None)
+        a = opt(xd, None)
+        b = opt(xd, torch.ones(x16.shape[:2], dtype=torch.bool, device=device))
+    ref = O.forward(O.params_fp32(gpu_model), x16.float(), None, w.config.num_heads, w.config.causal)
+    floor = O.check_tolerance(eager, ref, None)
+    ours = O.check_tolerance(a, ref, None)
+    print(f"[floor] eager fp16 {floor}  optimized {ours}", flush=True)
+    assert ours["passed"]
+    assert torch.equal(a, b)
+
+
+def test_stage_parity_layer0(device):
+    """Layer-0 intermediates of the kernel chain vs the oracle's stages (numerics localisation,
+    after benchmarks/benchmark_steps_1_2.py:73-117)."""
+    cfg = TransformerConfig(2, 128, 512, 8, 2048, 1, False)
+    model = build_model(cfg, seed=21)
+    x16, mask = make_inputs(cfg, True, 22)
+    gm = copy.deepcopy(model).half().to(device)
+    p32 = O.params_fp32(gm)
+    stages = {}
+    O.forward(p32, x16.float(), mask, cfg.num_heads, cfg.causal, stages=stages)
+    L = gm.layers[0]
+    xd, md = x16.to(device), mask.to(device)
+    ln1 = ops.layernorm(xd, L.norm1.weight, L.norm1.bias)
+    att = L.attention
+    wqkv = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight])
+    bqkv = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias])
+    q, k, vt = ops.qkv_projection(ln1, wqkv, bqkv, cfg.num_heads)
+    ctx = ops.attention(q, k, vt, md, cfg.causal)
+    x1 = ops.linear(ctx, att.out_proj.weight, att.out_proj.bias, "resid_masked", residual=xd, valid=md)
+    ln2 = ops.layernorm(x1, L.norm2.weight, L.norm2.bias)
+    hmid = ops.linear(ln2, L.ffn_in.weight, L.ffn_in.bias, "gelu")
+    x2 = ops.linear(hmid, L.ffn_out.weight, L.ffn_out.bias, "masked_resid", residual=x1, valid=md)
+    torch.cuda.synchronize()
+    v = mask
+    hd = 512 // 8
+    checks = {
+        "ln1": (ln1, stages["ln1"], 1e-2),
+        "q": (q.permute(0, 2, 1, 3).reshape(2, 128, 512), stages["q"], 2e-2),
+        "ctx": (ctx, stages["ctx"], 2e-2),
+        "x1": (x1, x16.float() + stages["attn_out"], 3e-2),
+        "gelu": (hmid, stages["gelu"], 2e-2),
+        "block_out": (x2, stages["block_out"], 4e-2),
+    }
+    for name, (got, want, tol) in checks.items():
+        err = (got.float().cpu()[v] - want[v]).abs().max().item()
+        assert err <= tol, (name, err)
+    assert (x2.cpu()[~v].view(torch.int16) == 0).all()
+    del hd

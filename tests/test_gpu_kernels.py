@@ -1,0 +1,232 @@
+"""Per-kernel parity of the HIP path (through the C ABI) against fp32 references on the same inputs.
+
+Tolerances: the kernels read fp16 inputs, accumulate in fp32 and round the output to fp16 once,
+so the references are computed in fp32 (on the CPU, from the same fp16 inputs) and the gate is a
+few fp16 ulps of the output magnitude (stated per test).  Padded rows must be bitwise +0.0.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import transformer_oracle as O
+from tttj_2026_amd import _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(shape, seed, scale=1.0, device="cuda"):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).half().to(device)
+
+
+def _bits_zero(t):
+    return bool((t.contiguous().view(torch.int16) == 0).all())
+
+
+# ---------------------------------------------------------------- LayerNorm
+@pytest.mark.parametrize("rows,d", [(1, 256), (3, 512), (1000, 1024), (77, 96), (5, 8192), (4096, 256)])
+def test_layernorm(device, rows, d):
+    x = _rand((rows, d), 1, scale=3.0) + 0.5
+    w = _rand((d,), 2, scale=0.3) + 1.0
+    b = _rand((d,), 3, scale=0.3)
+    valid = (torch.arange(rows) % 3 != 1).to(device)
+    y = ops.layernorm(x, w, b, valid)
+    torch.cuda.synchronize()
+    ref = O.layer_norm(x.float().cpu(), w.float().cpu(), b.float().cpu())
+    got = y.float().cpu()
+    v = valid.cpu()
+    err = (got[v] - ref[v]).abs().max().item()
+    assert err <= 4e-3 * max(1.0, ref.abs().max().item()), err
+    assert _bits_zero(y.cpu()[~v])
+    y2 = ops.layernorm(x, w, b, None)
+    assert (y2.float().cpu() - ref).abs().max().item() <= 4e-3 * max(1.0, ref.abs().max().item())
+
+
+# ---------------------------------------------------------------- GEMM + epilogues
+def _linear_ref(x, w, b):
+    return x.float().cpu() @ w.float().cpu().t() + b.float().cpu()
+
+
+GEMM_SHAPES = [(64, 768, 256), (100, 64, 64), (512, 1024, 256), (4096, 1536, 512),
+               (8192, 1024, 4096), (1, 128, 128), (300, 3072, 1024)]
+
+
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 3, 4])
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
+def test_linear_bias_all_tiles(device, m, n, k, tile):
+    if tile >= 0 and m * n * k > 2 ** 31:
+        pytest.skip("large shape covered by the automatic tile")
+    lib = _lib.load()
+    x = _rand((m, k), 10 + m, 1.0)
+    w = _rand((n, k), 11 + n, 1.0 / math.sqrt(k))
+    b = _rand((n,), 12, 0.5)
+    _lib.check(lib.tt_gemm_tile_override(tile), "override")
+    try:
+        y = ops.linear(x, w, b, "bias")
+        torch.cuda.synchronize()
+    finally:
+        lib.tt_gemm_tile_override(-1)
+    ref = _linear_ref(x, w, b)
+    err = (y.float().cpu() - ref).abs().max().item()
+    assert err <= 2e-3 * max(1.0, ref.abs().max().item()), (err, tile)
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 1024, 256), (8192, 4096, 1024), (37, 2048, 512)])
+def test_linear_gelu(device, m, n, k):
+    x = _rand((m, k), 20, 1.0)
+    w = _rand((n, k), 21, 1.0 / math.sqrt(k))
+    b = _rand((n,), 22, 0.5)
+    y = ops.linear(x, w, b, "gelu")
+    ref = O.gelu_erf(_linear_ref(x, w, b))
+    err = (y.float().cpu() - ref).abs().max().item()
+    assert err <= 2e-3 * max(1.0, ref.abs().max().item()), err
+
+
+@pytest.mark.parametrize("mode", ["resid_masked", "masked_resid"])
+@pytest.mark.parametrize("m,n,k", [(512, 256, 256), (4096, 512, 2048), (8192, 1024, 1024)])
+def test_linear_residual_epilogues(device, mode, m, n, k):
+    x = _rand((m, k), 30, 1.0)
+    w = _rand((n, k), 31, 1.0 / math.sqrt(k))
+    b = _rand((n,), 32, 0.5)
+    r = _rand((m, n), 33, 2.0)
+    valid = (torch.rand(m, generator=torch.Generator().manual_seed(34)) > 0.3).to(device)
+    ref_branch = _linear_ref(x, w, b)
+    rc, vc = r.float().cpu(), valid.cpu()[:, None]
+    if mode == "resid_masked":
+        ref = rc + torch.where(vc, ref_branch, torch.zeros(()))
+    else:
+        ref = torch.where(vc, rc + ref_branch, torch.zeros(()))
+    y = ops.linear(x, w, b, mode, residual=r, valid=valid)
+    err = (y.float().cpu() - ref).abs().max().item()
+    assert err <= 3e-3 * max(1.0, ref.abs().max().item()), err
+    if mode == "masked_resid":
+        assert _bits_zero(y.cpu()[~valid.cpu()])
+    # in place: residual aliases the output
+    r2 = r.clone()
+    ops.linear(x, w, b, mode, residual=r2, valid=valid, out=r2)
+    assert torch.equal(r2, y)
+
+
+def test_linear_rejects_bad_shapes(device):
+    x = _rand((64, 96), 1)
+    w = _rand((64, 96), 2)
+    b = _rand((64,), 3)
+    with pytest.raises(ValueError):
+        ops.linear(x, w, b)  # K = 96 is not a multiple of 64
+    x = _rand((64, 64), 1)
+    w = _rand((96, 64), 2)
+    with pytest.raises(ValueError):
+        ops.linear(x, w, _rand((96,), 3))  # N = 96 is not a multiple of 64
+
+
+# ---------------------------------------------------------------- QKV layout + attention
+@pytest.mark.parametrize("b,s,d,h", [(2, 64, 256, 8), (1, 100, 128, 2), (3, 128, 512, 8)])
+def test_qkv_projection_layout(device, b, s, d, h):
+    x = _rand((b, s, d), 40)
+    w = _rand((3 * d, d), 41, 1.0 / math.sqrt(d))
+    bias = _rand((3 * d,), 42, 0.5)
+    q, k, vt = ops.qkv_projection(x, w, bias, h)
+    torch.cuda.synchronize()
+    hd = d // h
+    ref = _linear_ref(x.reshape(-1, d), w, bias).reshape(b, s, 3, h, hd)
+    for got, want in ((q, ref[:, :, 0].permute(0, 2, 1, 3)), (k, ref[:, :, 1].permute(0, 2, 1, 3)),
+                      (vt[..., :s], ref[:, :, 2].permute(0, 2, 3, 1))):
+        err = (got.float().cpu() - want).abs().max().item()
+        assert err <= 2e-3 * max(1.0, want.abs().max().item()), err
+
+
+def _attention_ref(q, k, vt, mask, causal):
+    """fp32 CPU softmax(q k^T / sqrt(hd)) v with -inf masks; rows with no key -> 0."""
+    b, h, s, hd = q.shape
+    qf, kf = q.float().cpu(), k.float().cpu()
+    vf = vt[..., :s].float().cpu().transpose(-1, -2).contiguous()
+    sc = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) / math.sqrt(hd)
+    allowed = torch.ones(b, 1, s, s, dtype=torch.bool)
+    if causal:
+        allowed &= ~torch.ones(s, s, dtype=torch.bool).triu(1)
+    if mask is not None:
+        allowed &= mask.cpu()[:, None, None, :]
+    sc = sc.masked_fill(~allowed, float("-inf"))
+    p = torch.softmax(sc, dim=-1).nan_to_num(0.0)
+    return torch.matmul(p, vf).permute(0, 2, 1, 3).reshape(b, s, h * hd)
+
+
+def _masks(kind, b, s, seed):
+    g = torch.Generator().manual_seed(seed)
+    if kind == "none":
+        return None
+    if kind == "all":
+        return torch.ones(b, s, dtype=torch.bool)
+    if kind == "prefix":
+        lens = torch.randint(max(1, s // 2), s + 1, (b,), generator=g)
+        lens[0] = s
+        return torch.arange(s)[None, :] < lens[:, None]
+    if kind == "ragged_empty":
+        lens = torch.randint(0, s + 1, (b,), generator=g)
+        lens[-1] = 0
+        return torch.arange(s)[None, :] < lens[:, None]
+    m = torch.rand(b, s, generator=g) > 0.35  # non-prefix
+    m[:, 0] = True
+    return m
+
+
+@pytest.mark.parametrize("hd", [32, 64])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("s", [1, 37, 64, 128, 200, 512])
+@pytest.mark.parametrize("mask_kind", ["none", "prefix", "nonprefix", "ragged_empty"])
+def test_attention(device, hd, causal, s, mask_kind):
+    b, h = 3, 2
+    q = _rand((b, h, s, hd), 50 + s, 1.5)
+    k = _rand((b, h, s, hd), 51 + s, 1.5)
+    sp = (s + 63) // 64 * 64
+    vt = _rand((b, h, hd, sp), 52 + s, 1.0)
+    vt[..., s:] = float("nan")  # padding columns must never be read into the result
+    mask = _masks(mask_kind, b, s, 53 + s)
+    mdev = None if mask is None else mask.to(device)
+    ctx = ops.attention(q, k, vt, mdev, causal)
+    torch.cuda.synchronize()
+    ref = _attention_ref(q, k, vt, mask, causal)
+    got = ctx.float().cpu()
+    assert torch.isfinite(got).all()
+    if mask is not None:
+        assert _bits_zero(ctx.cpu()[~mask])
+        got, ref = got[mask], ref[mask]
+    if got.numel():
+        err = (got - ref).abs().max().item()
+        assert err <= 6e-3, err
+
+
+@pytest.mark.parametrize("b,s,h,hd,causal", [(2, 4096, 16, 64, True), (8, 1024, 16, 64, True),
+                                              (8, 512, 8, 64, False), (1, 64, 8, 32, True)])
+def test_attention_benchmark_shapes(device, b, s, h, hd, causal):
+    q = _rand((b, h, s, hd), 60, 1.0)
+    k = _rand((b, h, s, hd), 61, 1.0)
+    vt = _rand((b, h, hd, (s + 63) // 64 * 64), 62, 1.0)
+    mask = _masks("prefix", b, s, 63) if b == 8 else None
+    ctx = ops.attention(q, k, vt, None if mask is None else mask.to(device), causal)
+    torch.cuda.synchronize()
+    # spot-check two heads' worth of rows against the fp32 reference (full reference is large)
+    sl = slice(0, 1)
+    ref = _attention_ref(q[sl], k[sl], vt[sl], None if mask is None else mask[sl], causal)
+    got = ctx[sl].float().cpu()
+    if mask is not None:
+        got, ref = got[mask[sl]], ref[mask[sl]]
+    assert (got - ref).abs().max().item() <= 6e-3
+
+
+def test_attention_rejects_head_dim(device):
+    q = _rand((1, 1, 8, 16), 1)
+    vt = _rand((1, 1, 16, 64), 2)
+    with pytest.raises(ValueError):
+        ops.attention(q, q, vt, None, False)
+
+
+def test_mask_info(device):
+    mask = torch.tensor([[1, 1, 1, 0, 0], [1, 0, 1, 0, 0], [0, 0, 0, 0, 0], [1, 1, 1, 1, 1]],
+                        dtype=torch.bool)
+    info = ops.mask_info(mask.to(device), 4, 5, device).cpu().tolist()
+    assert info == [3, 3, 0, 5, 1, 0, 1, 1]
+    info = ops.mask_info(None, 2, 7, device).cpu().tolist()
+    assert info == [7, 7, 1, 1]

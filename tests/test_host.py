@@ -1,0 +1,103 @@
+"""CPU tests of the host side: C-ABI exports, layout bookkeeping, config validation, packing rules.
+
+None of these launch a kernel; the library's bookkeeping exports run without a GPU.
+"""
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+import torch
+
+from tttj_2026_amd import _lib, check_supported, make_optimized_transformer
+from tttj_2026_amd.configs import WORKLOADS, build_model
+from tttj_2026_amd.model import TransformerConfig
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "tttj_amd.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(tt_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _declared_functions()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), name
+    # the Python binding declares exactly the header's functions
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_version_and_error_channel():
+    lib = _lib.load()
+    assert b"gfx950" in lib.tt_version()
+    rc = lib.tt_weight_layout(0, 1, 1, None, None, None, None)
+    assert rc == _lib.TT_ERR_INVALID
+    assert "bad shape" in _lib.last_error()
+
+
+def test_weight_layout_matches_definition():
+    for name in WORKLOADS:
+        cfg = WORKLOADS[name].config
+        d, f, n = cfg.d_model, cfg.ffn_dim, cfg.num_layers
+        offs, stride, final, total = _lib.weight_layout(d, f, n)
+        sizes = [d, d, 3 * d * d, 3 * d, d * d, d, d, d, f * d, f, d * f, d]
+        al = lambda v: (v + 63) // 64 * 64
+        o = 0
+        for i, s in enumerate(sizes):
+            assert offs[i] == o and o % 64 == 0
+            o += al(s)
+        assert stride == o and final == n * stride and total == final + 2 * al(d)
+
+
+def test_workspace_bytes_monotone_and_validated():
+    small = _lib.workspace_bytes(1, 64, 256, 8, 1024)
+    big = _lib.workspace_bytes(2, 4096, 1024, 16, 4096)
+    assert 0 < small < big
+    # C5 workspace: x, LN/ctx, Q, K, V^T, FFN hidden (fp16) ~ 144 MiB
+    assert big == pytest.approx((4 * 8192 * 1024 + 2 * 1024 * 4096 + 8192 * 4096) * 2, rel=1e-3)
+    with pytest.raises(ValueError):
+        _lib.workspace_bytes(1, 64, 256, 16, 1024)  # head_dim 16
+
+
+@pytest.mark.parametrize("kwargs,ok", [
+    (dict(d_model=256, num_heads=8, ffn_dim=1024), True),     # hd 32
+    (dict(d_model=1024, num_heads=16, ffn_dim=4096), True),   # hd 64
+    (dict(d_model=128, num_heads=4, ffn_dim=128), True),      # the reference's own D=F shape
+    (dict(d_model=256, num_heads=16, ffn_dim=1024), False),   # hd 16
+    (dict(d_model=512, num_heads=4, ffn_dim=2048), False),    # hd 128
+    (dict(d_model=96, num_heads=3, ffn_dim=128), False),      # D not a multiple of 64
+    (dict(d_model=256, num_heads=4, ffn_dim=1000), False),    # F not a multiple of 64
+])
+def test_check_supported(kwargs, ok):
+    cfg = TransformerConfig(batch_size=2, seq_len=16, num_layers=2, causal=True, **kwargs)
+    if ok:
+        check_supported(cfg)
+    else:
+        with pytest.raises(ValueError, match="no optimized transformer"):
+            check_supported(cfg)
+
+
+def test_make_optimized_requires_gpu_fp16_params():
+    model = build_model(WORKLOADS["C2"].config)  # fp32 on the CPU
+    with pytest.raises(ValueError, match="CUDA float16"):
+        make_optimized_transformer(model)
+
+
+def test_c_abi_rejects_bad_arguments_without_launching():
+    lib = _lib.load()
+    # null pointers and unsupported shapes are refused before any HIP call
+    assert lib.tt_transformer_fwd(None, None, None, None, None, 0, 1, 64, 256, 8, 1024, 1, 1, 0,
+                                  None) == _lib.TT_ERR_INVALID
+    assert lib.tt_linear_fwd(None, None, None, None, None, None, 64, 64, 64, 0, 0, 0, 0,
+                             None) == _lib.TT_ERR_INVALID
+    assert lib.tt_attention_fwd(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                None, None, ctypes.c_void_p(16), 1, 8, 1, 48, 0,
+                                None) == _lib.TT_ERR_INVALID
+    assert "head_dim" in _lib.last_error()
+    assert lib.tt_gemm_tile_override(99) == _lib.TT_ERR_INVALID

@@ -1,0 +1,29 @@
+"""MI355X-native (gfx950) optimized forward pass for the pre-LN transformer block stack.
+
+Drop-in for the reference's ``make_optimized_transformer(model)`` / ``forward(x, valid_token_mask)``
+(optimized_transformer.py:69-93): hand-written HIP kernels behind a C ABI (include/tttj_amd.h),
+loaded with ctypes; PyTorch-ROCm provides device memory and streams.
+"""
+
+from .model import BaselineTransformer, TransformerConfig
+from .optimized_transformer import (
+    PLAN_AUTO,
+    PLAN_LAYERWISE,
+    PLAN_MEGAKERNEL,
+    OptimizedTransformer,
+    check_supported,
+    make_optimized_transformer,
+    pack_model_weights,
+)
+
+__all__ = [
+    "BaselineTransformer",
+    "TransformerConfig",
+    "OptimizedTransformer",
+    "make_optimized_transformer",
+    "pack_model_weights",
+    "check_supported",
+    "PLAN_AUTO",
+    "PLAN_LAYERWISE",
+    "PLAN_MEGAKERNEL",
+]

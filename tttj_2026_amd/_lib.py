@@ -1,0 +1,94 @@
+"""ctypes binding of the C ABI declared in ``include/tttj_amd.h`` (library ``libtttj_amd.so``).
+
+There is no fallback: if the library is missing or fails to load, every optimized entry point
+raises.  Loading needs no GPU (the bookkeeping exports work on a CPU-only host); the compute
+exports need a gfx950 device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import threading
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "libtttj_amd.so"
+
+TT_OK, TT_ERR_INVALID, TT_ERR_HIP = 0, 1, 2
+EPILOGUES = {"bias": 0, "gelu": 1, "resid_masked": 2, "masked_resid": 3, "qkv": 4}
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+
+# name -> (restype, argtypes); must match include/tttj_amd.h exactly.
+SIGNATURES = {
+    "tt_version": (ctypes.c_char_p, []),
+    "tt_last_error_string": (ctypes.c_char_p, []),
+    "tt_device_count": (_I, []),
+    "tt_weight_layout": (_I, [_I, _I, _I, ctypes.POINTER(_I64), ctypes.POINTER(_I64),
+                              ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
+    "tt_workspace_bytes": (_I, [_I, _I, _I, _I, _I, ctypes.POINTER(_I64)]),
+    "tt_layernorm_fwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _P]),
+    "tt_linear_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "tt_gemm_tile_override": (_I, [_I]),
+    "tt_mask_info": (_I, [_P, _P, _I, _I, _P]),
+    "tt_attention_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "tt_transformer_fwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class LibraryError(RuntimeError):
+    pass
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library with typed signatures."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise LibraryError(
+                    f"{LIB_PATH} is not built; run `python -m tttj_2026_amd.build` "
+                    "(or __graft_entry__.build()) first")
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+        return _lib
+
+
+def last_error() -> str:
+    return load().tt_last_error_string().decode(errors="replace")
+
+
+def check(rc: int, what: str) -> None:
+    """Raise for a non-zero status: ValueError for argument errors, RuntimeError for HIP errors."""
+    if rc == TT_OK:
+        return
+    msg = f"{what}: {last_error()}"
+    if rc == TT_ERR_INVALID:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def weight_layout(d_model: int, ffn_dim: int, num_layers: int):
+    """Return (12 per-layer offsets, layer stride, final-norm offset, total elements)."""
+    lib = load()
+    offs = (_I64 * 12)()
+    stride, final, total = _I64(), _I64(), _I64()
+    check(lib.tt_weight_layout(d_model, ffn_dim, num_layers, offs, ctypes.byref(stride),
+                               ctypes.byref(final), ctypes.byref(total)), "tt_weight_layout")
+    return list(offs), stride.value, final.value, total.value
+
+
+def workspace_bytes(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int) -> int:
+    out = _I64()
+    check(load().tt_workspace_bytes(batch, seq, d_model, heads, ffn_dim, ctypes.byref(out)),
+          "tt_workspace_bytes")
+    return out.value

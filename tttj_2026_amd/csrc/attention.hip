@@ -1,0 +1,311 @@
+// Flash attention (online softmax) for head_dim 32 and 64 on gfx950, plus the per-sequence mask
+// summary it and the executor use.
+//
+// One 256-thread block owns (sequence b, head h, 128-query tile); each of its four waves owns 32
+// queries.  Key/value tiles of 64 keys are staged in LDS (double-buffered, register prefetch of
+// the next tile during the current tile's math).  Per wave and tile:
+//   S^T = K Q^T   with v_mfma_f32_32x32x16_f16 (K from LDS as the A operand, Q^T held in
+//                 registers as the B operand), so lane l holds one query (l % 32) and 32 of the 64
+//                 keys: the row max needs a single cross-half exchange (lane ^ 32) and the row sum
+//                 stays lane-partial until the end;
+//   O^T += V^T P^T with V^T tiles from LDS (the QKV projection writes V transposed, [hd, S]).
+// To make the probabilities a lane already holds line up with 8 consecutive keys of V^T, the K
+// tile rows are placed in LDS with bits 2 and 3 of the row index swapped: S^T row r then holds
+// key pi(r), and lane l of key block kb holds keys 32kb + 16(j/8) + 8(l/32) + (j%8), j = 0..15.
+// Softmax runs in the exp2 domain with scale*log2(e) folded into one FMA per score.  Masking:
+// keys are dropped when key >= kv_end (last valid key + 1), when causal && key > query, and, for
+// masks that are not right-padded prefixes, when mask[b, key] == 0.  Query rows that are padded
+// are written as +0.0.  Causal query tiles are scheduled heaviest-first.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace tt {
+
+constexpr int kBQ = 128;
+constexpr int kBKV = 64;
+
+__host__ __device__ constexpr int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+__device__ __forceinline__ int pi23(int r) {  // swap bits 2 and 3
+  return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
+}
+
+// chunk swizzle for a K tile row of HD halfs (HD/8 chunks of 16 bytes)
+template <int HD>
+__device__ __forceinline__ int kswz(int row, int c) {
+  if constexpr (HD == 64) return c ^ (row & 7);
+  else return c ^ ((row >> 1) & 3);
+}
+
+template <int HD, bool CAUSAL>
+__global__ __launch_bounds__(256) void attention_kernel(
+    const half* __restrict__ Q, const half* __restrict__ K, const half* __restrict__ Vt,
+    const uint8_t* __restrict__ mask, const int32_t* __restrict__ info, half* __restrict__ ctx,
+    int B, int S, int H, float scale_log2) {
+  constexpr int KSTEPS = HD / 16;  // k-steps of the S^T MFMA
+  constexpr int DB = HD / 32;      // 32-row blocks of O^T
+  constexpr int KCH = HD / 8;      // 16-byte chunks per K row
+  constexpr int KPT = kBKV * KCH / 256;
+  constexpr int VPT = HD * 8 / 256;
+  static_assert(KPT >= 1 && VPT >= 1, "tile too small for the block");
+
+  __shared__ __align__(16) half sk[2][kBKV * HD];
+  __shared__ __align__(16) half sv[2][HD * kBKV];
+
+  const int BH = B * H;
+  const int nqt = (S + kBQ - 1) / kBQ;
+  const int bh = blockIdx.x % BH;
+  int qt = blockIdx.x / BH;
+  if (CAUSAL) qt = nqt - 1 - qt;
+  const int b = bh / H, h = bh - b * H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hf = lane >> 5, col = lane & 31;
+  const int ldv = round_up(S, kBKV);
+
+  int kv_end = S;
+  bool prefix = true;
+  if (info != nullptr) {
+    kv_end = info[b];
+    prefix = info[B + b] != 0;
+  }
+  const bool keymask = (mask != nullptr) && !prefix;
+
+  const int q0 = qt * kBQ;
+  const int qw = q0 + wave * 32;
+  const int q = qw + col;
+  const int block_end = CAUSAL ? min(kv_end, q0 + kBQ) : kv_end;
+  const int ntiles = (block_end + kBKV - 1) / kBKV;
+  const bool wave_active = qw < kv_end;  // queries >= kv_end are padded
+  const int wave_end = CAUSAL ? min(kv_end, qw + 32) : kv_end;
+
+  const size_t D = (size_t)H * HD;
+  const half* Qbh = Q + (size_t)bh * S * HD;
+  const half* Kbh = K + (size_t)bh * S * HD;
+  const half* Vbh = Vt + (size_t)bh * HD * ldv;
+
+  half8 qf[KSTEPS];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) {
+    if (q < S) qf[kk] = *(const half8*)(Qbh + (size_t)q * HD + 16 * kk + 8 * hf);
+    else
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[kk][e] = (half)0.f;
+  }
+
+  floatx16 o[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[i][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  uint4 rk[KPT], rv[VPT];
+  auto gload = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int id = tid + 256 * i, r = id / KCH, c = id % KCH, key = t0 + r;
+      rk[i] = key < S ? *(const uint4*)(Kbh + (size_t)key * HD + c * 8) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int id = tid + 256 * i, d = id >> 3, c = id & 7, key = t0 + 8 * c;
+      uint4 v = *(const uint4*)(Vbh + (size_t)d * ldv + key);  // in bounds: rows padded to ldv
+      if (key + 8 > S) {
+        half8 hv = *(half8*)&v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (key + e >= S) hv[e] = (half)0.f;
+        v = *(uint4*)&hv;
+      }
+      rv[i] = v;
+    }
+  };
+  auto lstore = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int id = tid + 256 * i, r = id / KCH, c = id % KCH;
+      const int pos = (r & ~31) | pi23(r & 31);
+      *(uint4*)(&sk[st][pos * HD + kswz<HD>(pos, c) * 8]) = rk[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int id = tid + 256 * i, d = id >> 3, c = id & 7;
+      *(uint4*)(&sv[st][d * kBKV + swz(d, c) * 8]) = rv[i];
+    }
+  };
+
+  if (ntiles > 0) {
+    gload(0);
+    lstore(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int st = t & 1;
+    const int t0 = t * kBKV;
+    if (t + 1 < ntiles) gload(t0 + kBKV);
+    if (wave_active && t0 < wave_end) {
+      floatx16 s[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
+        const int row = kb * 32 + col;
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; ++kk) {
+          const half8 a = *(const half8*)(&sk[st][row * HD + kswz<HD>(row, 2 * kk + hf) * 8]);
+          s[kb] = mfma32x32x16(a, qf[kk], s[kb]);
+        }
+      }
+      const bool need_mask = (t0 + kBKV > kv_end) || (CAUSAL && t0 + kBKV - 1 > qw) || keymask;
+      if (need_mask) {
+        uint64_t kbits = ~0ull;
+        if (keymask) {
+          const int key = t0 + lane;
+          kbits = __ballot(key < S && mask[(size_t)b * S + key] != 0);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int kr = 32 * kb + 16 * (j >> 3) + 8 * hf + (j & 7);
+            const int key = t0 + kr;
+            const bool ok = key < kv_end && (!CAUSAL || key <= q) && ((kbits >> kr) & 1ull);
+            if (!ok) s[kb][j] = -INFINITY;
+          }
+      }
+      float mx = s[0][0];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[kb][j]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx);
+      const float mc = (m_new == -INFINITY) ? 0.f : m_new * scale_log2;
+      const float corr = __builtin_amdgcn_exp2f(m_run * scale_log2 - mc);
+      m_run = m_new;
+      float psum = 0.f;
+      half8 p16[2][2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][j], scale_log2, -mc));
+          psum += p;
+          p16[kb][j >> 3][j & 7] = (half)p;
+        }
+      l_run = l_run * corr + psum;
+#pragma unroll
+      for (int i = 0; i < DB; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[i][e] *= corr;
+#pragma unroll
+      for (int i = 0; i < DB; ++i) {
+        const int row = i * 32 + col;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const half8 a = *(const half8*)(&sv[st][row * kBKV + swz(row, 4 * kb + 2 * c + hf) * 8]);
+            o[i] = mfma32x32x16(a, p16[kb][c], o[i]);
+          }
+      }
+    }
+    if (t + 1 < ntiles) lstore(st ^ 1);
+    __syncthreads();
+  }
+
+  if (q >= S) return;
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const bool qvalid = wave_active && q < kv_end && (mask == nullptr || mask[(size_t)b * S + q] != 0);
+  const float inv = (qvalid && l_tot > 0.f) ? 1.0f / l_tot : 0.f;
+  half* dst = ctx + ((size_t)b * S + q) * D + (size_t)h * HD;
+#pragma unroll
+  for (int i = 0; i < DB; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * i + 8 * g + 4 * hf;
+      half4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (half)(o[i][4 * g + e] * inv);
+      *(half4*)(dst + d) = v;
+    }
+}
+
+__global__ __launch_bounds__(256) void mask_info_kernel(const uint8_t* __restrict__ mask,
+                                                        int32_t* __restrict__ info, int B, int S) {
+  const int b = blockIdx.x;
+  int last = -1, count = 0;
+  if (mask == nullptr) {
+    last = S - 1;
+    count = S;
+  } else {
+    for (int s = threadIdx.x; s < S; s += 256)
+      if (mask[(size_t)b * S + s]) {
+        last = s;
+        ++count;
+      }
+  }
+  __shared__ int sl[256], sc[256];
+  sl[threadIdx.x] = last;
+  sc[threadIdx.x] = count;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if ((int)threadIdx.x < off) {
+      sl[threadIdx.x] = max(sl[threadIdx.x], sl[threadIdx.x + off]);
+      sc[threadIdx.x] += sc[threadIdx.x + off];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (mask == nullptr) {
+      info[b] = S;
+      info[B + b] = 1;
+    } else {
+      info[b] = sl[0] + 1;
+      info[B + b] = (sc[0] == sl[0] + 1) ? 1 : 0;
+    }
+  }
+}
+
+int launch_mask_info(const uint8_t* mask, int32_t* info, int batch, int seq, hipStream_t stream) {
+  TT_REQUIRE(batch > 0 && seq > 0 && info != nullptr, "mask_info: bad arguments");
+  hipLaunchKernelGGL(mask_info_kernel, dim3(batch), dim3(256), 0, stream, mask, info, batch, seq);
+  return launch_status("mask_info_kernel");
+}
+
+int launch_attention(const half* q, const half* k, const half* vt, const uint8_t* mask,
+                     const int32_t* info, half* ctx, int batch, int seq, int heads, int head_dim,
+                     int causal, hipStream_t stream) {
+  TT_REQUIRE(batch > 0 && seq > 0 && heads > 0, "attention: bad shape");
+  TT_REQUIRE(head_dim == 32 || head_dim == 64, "attention: head_dim %d not in {32, 64}", head_dim);
+  TT_REQUIRE(mask == nullptr || info != nullptr, "attention: a mask needs its mask_info");
+  const long blocks = (long)batch * heads * ((seq + kBQ - 1) / kBQ);
+  TT_REQUIRE(blocks < (1L << 31), "attention: grid too large");
+  const float scale_log2 = (1.0f / sqrtf((float)head_dim)) * 1.4426950408889634f;
+  const dim3 grid((unsigned)blocks), block(256);
+#define TT_ATT(HD, C)                                                                         \
+  hipLaunchKernelGGL((attention_kernel<HD, C>), grid, block, 0, stream, q, k, vt, mask, info, \
+                     ctx, batch, seq, heads, scale_log2)
+  if (head_dim == 64) {
+    if (causal) TT_ATT(64, true); else TT_ATT(64, false);
+  } else {
+    if (causal) TT_ATT(32, true); else TT_ATT(32, false);
+  }
+#undef TT_ATT
+  return launch_status("attention_kernel");
+}
+
+}  // namespace tt
+
+extern "C" int tt_mask_info(const uint8_t* mask, int32_t* info, int batch, int seq, void* stream) {
+  return tt::launch_mask_info(mask, info, batch, seq, (hipStream_t)stream);
+}
+
+extern "C" int tt_attention_fwd(const void* q, const void* k, const void* vt, const uint8_t* mask,
+                                const int32_t* info, void* ctx, int batch, int seq, int heads,
+                                int head_dim, int causal, void* stream) {
+  TT_REQUIRE(q && k && vt && ctx, "attention: null pointer");
+  return tt::launch_attention((const tt::half*)q, (const tt::half*)k, (const tt::half*)vt, mask,
+                              info, (tt::half*)ctx, batch, seq, heads, head_dim, causal,
+                              (hipStream_t)stream);
+}

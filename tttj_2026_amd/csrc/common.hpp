@@ -1,0 +1,72 @@
+// Shared device/host helpers for the gfx950 kernels of the pre-LN transformer forward.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "tttj_amd.h"
+
+namespace tt {
+
+using half = _Float16;
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWave = 64;
+
+// ---- error reporting across the C ABI (no exceptions cross it) ----
+void set_error(const std::string& msg);
+int fail(int code, const char* fmt, ...);
+
+#define TT_HIP(call)                                                                   \
+  do {                                                                                 \
+    hipError_t e_ = (call);                                                            \
+    if (e_ != hipSuccess)                                                              \
+      return ::tt::fail(TT_ERR_HIP, "%s failed: %s", #call, hipGetErrorString(e_));   \
+  } while (0)
+
+#define TT_REQUIRE(cond, ...)                                                          \
+  do {                                                                                 \
+    if (!(cond)) return ::tt::fail(TT_ERR_INVALID, __VA_ARGS__);                       \
+  } while (0)
+
+inline int launch_status(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TT_ERR_HIP, "launch of %s failed: %s", what, hipGetErrorString(e));
+  return TT_OK;
+}
+
+// ---- device helpers ----
+__device__ __forceinline__ floatx16 mfma32x32x16(half8 a, half8 b, floatx16 c) {
+  // v_mfma_f32_32x32x16_f16.  Lane l supplies A[row = l%32][k = 8*(l/32) + i] and
+  // B[k = 8*(l/32) + i][col = l%32]; it receives C[row = 8*(j/4) + 4*(l/32) + j%4][col = l%32].
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ floatx4 mfma16x16x32(half8 a, half8 b, floatx4 c) {
+  // v_mfma_f32_16x16x32_f16.  Lane l supplies A[row = l%16][k = 8*(l/16) + i] and
+  // B[k = 8*(l/16) + i][col = l%16]; it receives C[row = 4*(l/16) + j][col = l%16].
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float gelu_erf(float v) {
+  // Exact GELU, F.gelu(approximate="none"): 0.5 v (1 + erf(v / sqrt 2)).
+  return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+}
+
+// 16-byte element chunk index swizzle for [rows][64 halfs] LDS tiles (128-byte rows): XOR with the
+// row's low three bits so that the eight lanes of one ds_read_b128 phase, which read eight
+// consecutive rows at the same logical chunk, hit eight different 16-byte bank groups.
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (row & 7); }
+
+}  // namespace tt

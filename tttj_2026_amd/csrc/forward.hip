@@ -1,0 +1,199 @@
+// Forward executor and the C-ABI bookkeeping entry points (layout, workspace, errors, version).
+//
+// tt_transformer_fwd runs the whole block stack in one C call on the caller's stream, so a
+// forward costs one host->library crossing whatever the layer count:
+//   mask_info (only with a mask)
+//   per layer: LN1 -> QKV GEMM (head-major Q/K, transposed V) -> flash attention
+//              -> out_proj GEMM (+bias, masked branch, residual)  -> LN2
+//              -> ffn_in GEMM (+bias, exact GELU) -> ffn_out GEMM (+bias, residual, row mask)
+//   final LN (+row mask) into y.
+// The caller's x is read, never written; the residual stream lives in the workspace.
+#include "common.hpp"
+#include "kernels.hpp"
+
+#include <cstdarg>
+#include <cstring>
+
+namespace tt {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+static int64_t align64(int64_t v) { return (v + 63) / 64 * 64; }
+static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+struct Layout {
+  int64_t off[12];
+  int64_t stride, final_off, total;
+};
+
+static Layout weight_layout(int64_t D, int64_t F, int64_t L) {
+  const int64_t sizes[12] = {D, D, 3 * D * D, 3 * D, D * D, D, D, D, F * D, F, D * F, D};
+  Layout lay{};
+  int64_t o = 0;
+  for (int i = 0; i < 12; ++i) {
+    lay.off[i] = o;
+    o += align64(sizes[i]);
+  }
+  lay.stride = o;
+  lay.final_off = L * o;
+  lay.total = lay.final_off + 2 * align64(D);
+  return lay;
+}
+
+struct Workspace {
+  half *xa, *xn, *qkv, *hbuf;
+  int32_t* info;
+  size_t bytes;
+};
+
+static Workspace carve(char* base, int64_t B, int64_t S, int64_t D, int64_t F) {
+  const int64_t T = B * S, Sp = (S + 63) / 64 * 64;
+  Workspace w{};
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base ? base + o : nullptr;
+    o += align256(bytes);
+    return p;
+  };
+  w.xa = (half*)take(T * D * 2);
+  w.xn = (half*)take(T * D * 2);  // LN output, then attention context, then LN2 output
+  w.qkv = (half*)take((2 * T * D + B * D * Sp) * 2);
+  w.hbuf = (half*)take(T * F * 2);
+  w.info = (int32_t*)take(2 * B * 4);
+  w.bytes = o;
+  return w;
+}
+
+static int check_model_shape(int B, int S, int D, int H, int F, int L) {
+  TT_REQUIRE(B > 0 && S > 0 && D > 0 && H > 0 && F > 0 && L > 0,
+             "transformer: non-positive shape B=%d S=%d D=%d H=%d F=%d L=%d", B, S, D, H, F, L);
+  TT_REQUIRE(D % H == 0, "transformer: d_model %d not divisible by heads %d", D, H);
+  TT_REQUIRE(D / H == 32 || D / H == 64, "transformer: head_dim %d not in {32, 64}", D / H);
+  TT_REQUIRE(D % 64 == 0 && F % 64 == 0, "transformer: d_model %d and ffn_dim %d must be multiples of 64", D, F);
+  TT_REQUIRE(D <= 8192, "transformer: d_model %d > 8192", D);
+  TT_REQUIRE((int64_t)B * S < (1LL << 31) / 8, "transformer: too many tokens");
+  return TT_OK;
+}
+
+}  // namespace tt
+
+using namespace tt;
+
+extern "C" const char* tt_version(void) { return "tttj_amd 0.1 gfx950"; }
+
+extern "C" const char* tt_last_error_string(void) { return g_last_error.c_str(); }
+
+extern "C" int tt_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return -1;
+  return n;
+}
+
+extern "C" int tt_weight_layout(int d_model, int ffn_dim, int num_layers,
+                                int64_t layer_offsets[12], int64_t* layer_stride,
+                                int64_t* final_norm_offset, int64_t* total_elems) {
+  TT_REQUIRE(d_model > 0 && ffn_dim > 0 && num_layers > 0, "weight_layout: bad shape");
+  const Layout lay = weight_layout(d_model, ffn_dim, num_layers);
+  if (layer_offsets) memcpy(layer_offsets, lay.off, sizeof(lay.off));
+  if (layer_stride) *layer_stride = lay.stride;
+  if (final_norm_offset) *final_norm_offset = lay.final_off;
+  if (total_elems) *total_elems = lay.total;
+  return TT_OK;
+}
+
+extern "C" int tt_workspace_bytes(int batch, int seq, int d_model, int num_heads, int ffn_dim,
+                                  int64_t* bytes) {
+  int rc = check_model_shape(batch, seq, d_model, num_heads, ffn_dim, 1);
+  if (rc != TT_OK) return rc;
+  TT_REQUIRE(bytes != nullptr, "workspace_bytes: null output");
+  *bytes = (int64_t)carve(nullptr, batch, seq, d_model, ffn_dim).bytes;
+  return TT_OK;
+}
+
+extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint8_t* mask, void* y,
+                                  void* workspace, int64_t workspace_bytes, int batch, int seq,
+                                  int d_model, int num_heads, int ffn_dim, int num_layers,
+                                  int causal, int plan, void* stream_) {
+  int rc = check_model_shape(batch, seq, d_model, num_heads, ffn_dim, num_layers);
+  if (rc != TT_OK) return rc;
+  TT_REQUIRE(weights && x && y && workspace, "transformer: null pointer");
+  TT_REQUIRE(x != y, "transformer: y must not alias x");
+  TT_REQUIRE(plan == 0 || plan == 1, "transformer: plan %d not available", plan);
+  const int B = batch, S = seq, D = d_model, H = num_heads, F = ffn_dim, L = num_layers;
+  const int T = B * S, hd = D / H;
+  Workspace ws = carve((char*)workspace, B, S, D, F);
+  TT_REQUIRE((int64_t)ws.bytes <= workspace_bytes, "transformer: workspace %lld < %zu bytes",
+             (long long)workspace_bytes, ws.bytes);
+  const hipStream_t stream = (hipStream_t)stream_;
+  const Layout lay = weight_layout(D, F, L);
+  const half* wts = (const half*)weights;
+  const size_t plane = (size_t)T * D;
+  half* q = ws.qkv;
+  half* k = ws.qkv + plane;
+  half* vt = ws.qkv + 2 * plane;
+  const int32_t* info = nullptr;
+  if (mask != nullptr) {
+    if ((rc = launch_mask_info(mask, ws.info, B, S, stream)) != TT_OK) return rc;
+    info = ws.info;
+  }
+  const half* cur = (const half*)x;
+  for (int l = 0; l < L; ++l) {
+    const half* w = wts + (size_t)l * lay.stride;
+    if ((rc = launch_layernorm(cur, w + lay.off[0], w + lay.off[1], nullptr, ws.xn, T, D, 1e-5f,
+                               stream)) != TT_OK)
+      return rc;
+    EpiArgs ep{};
+    ep.bias = w + lay.off[3];
+    ep.y = q;
+    ep.ldy = 3 * D;
+    ep.mode = TT_EPI_QKV;
+    ep.batch = B;
+    ep.seq = S;
+    ep.heads = H;
+    ep.head_dim = hd;
+    ep.d_model = D;
+    if ((rc = launch_linear(ws.xn, w + lay.off[2], T, 3 * D, D, ep, stream)) != TT_OK) return rc;
+    if ((rc = launch_attention(q, k, vt, mask, info, ws.xn, B, S, H, hd, causal, stream)) != TT_OK)
+      return rc;
+    ep = EpiArgs{};
+    ep.bias = w + lay.off[5];
+    ep.resid = cur;
+    ep.valid = mask;
+    ep.y = ws.xa;
+    ep.ldy = D;
+    ep.mode = TT_EPI_RESID_MASKED;
+    if ((rc = launch_linear(ws.xn, w + lay.off[4], T, D, D, ep, stream)) != TT_OK) return rc;
+    if ((rc = launch_layernorm(ws.xa, w + lay.off[6], w + lay.off[7], nullptr, ws.xn, T, D, 1e-5f,
+                               stream)) != TT_OK)
+      return rc;
+    ep = EpiArgs{};
+    ep.bias = w + lay.off[9];
+    ep.y = ws.hbuf;
+    ep.ldy = F;
+    ep.mode = TT_EPI_BIAS_GELU;
+    if ((rc = launch_linear(ws.xn, w + lay.off[8], T, F, D, ep, stream)) != TT_OK) return rc;
+    ep = EpiArgs{};
+    ep.bias = w + lay.off[11];
+    ep.resid = ws.xa;
+    ep.valid = mask;
+    ep.y = ws.xa;
+    ep.ldy = D;
+    ep.mode = TT_EPI_MASKED_RESID;
+    if ((rc = launch_linear(ws.hbuf, w + lay.off[10], T, D, F, ep, stream)) != TT_OK) return rc;
+    cur = ws.xa;
+  }
+  return launch_layernorm(cur, wts + lay.final_off, wts + lay.final_off + align64(D), mask,
+                          (half*)y, T, D, 1e-5f, stream);
+}

@@ -1,0 +1,171 @@
+"""Public construction API: ``make_optimized_transformer(model)`` -> module with ``forward(x, mask)``.
+
+Drop-in for ``optimized_transformer.make_optimized_transformer`` (optimized_transformer.py:69-93):
+the same signature and the same ``forward(x, valid_token_mask=None)`` contract
+(kernels/sequence_resident.py:227-233).  Instead of the reference's table of 14 fixed shapes
+(optimized_transformer.py:22-66) any configuration with ``head_dim in {32, 64}`` and ``d_model``,
+``ffn_dim`` multiples of 64 is accepted, causal or not; anything else raises ``ValueError`` before
+any work, as the reference does for unsupported shapes.
+
+The module packs the parameter model's fp16 weights once (``prepare``) into the layout of
+``tt_weight_layout`` and runs every forward as one call into the HIP library on the caller's
+current stream.  It returns a fresh output tensor per call; repeated calls on the same inputs are
+bit-identical.  A module instance owns one workspace per (batch, seq) and is not re-entrant across
+streams.
+"""
+
+from __future__ import annotations
+
+from typing import Dict, Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+
+PLAN_AUTO, PLAN_LAYERWISE, PLAN_MEGAKERNEL = 0, 1, 2
+
+
+def check_supported(config) -> None:
+    """Raise ValueError unless the HIP path implements ``config`` (a TransformerConfig-like)."""
+    d, h, f = config.d_model, config.num_heads, config.ffn_dim
+    problems = []
+    if min(config.batch_size, config.seq_len, d, h, f, config.num_layers) <= 0:
+        problems.append("all sizes must be positive")
+    elif d % h != 0:
+        problems.append(f"d_model {d} not divisible by num_heads {h}")
+    else:
+        if d // h not in (32, 64):
+            problems.append(f"head_dim {d // h} not in (32, 64)")
+        if d % 64 or f % 64:
+            problems.append("d_model and ffn_dim must be multiples of 64")
+        if d > 8192:
+            problems.append("d_model must be <= 8192")
+    if problems:
+        raise ValueError(
+            "no optimized transformer is implemented for "
+            f"shape={(config.batch_size, config.seq_len, d, h)}, ffn_dim={f}, "
+            f"layers={config.num_layers}, causal={config.causal}: " + "; ".join(problems))
+
+
+def pack_model_weights(model: nn.Module) -> torch.Tensor:
+    """Pack ``model``'s parameters into one contiguous fp16 buffer in the C-ABI layout.
+
+    Generalises kernels/sequence_resident.py:74-109 (F == D only) to any F; q, k and v weights and
+    biases are concatenated into one [3D, D] projection.  Segment offsets come from the library
+    (``tt_weight_layout``) so Python and C cannot disagree about the layout.
+    """
+    cfg = model.config
+    d, f, n_layers = cfg.d_model, cfg.ffn_dim, cfg.num_layers
+    offs, stride, final, total = _lib.weight_layout(d, f, n_layers)
+    ref = model.final_norm.weight
+    if ref.device.type != "cuda" or ref.dtype != torch.float16:
+        raise ValueError("parameters must be CUDA float16 before prepare()")
+    packed = torch.zeros(total, dtype=torch.float16, device=ref.device)
+
+    def put(base: int, seg: int, *tensors: torch.Tensor) -> None:
+        o = base + offs[seg]
+        for t in tensors:
+            t = t.detach()
+            if t.dtype != torch.float16 or t.device != ref.device:
+                raise ValueError("all parameters must be CUDA float16 on one device")
+            packed[o:o + t.numel()].copy_(t.reshape(-1))
+            o += t.numel()
+
+    for i, layer in enumerate(model.layers):
+        base = i * stride
+        att = layer.attention
+        for lin in (att.q_proj, att.k_proj, att.v_proj, att.out_proj, layer.ffn_in, layer.ffn_out):
+            if lin.bias is None:
+                raise ValueError("every projection must have a bias")
+        put(base, 0, layer.norm1.weight)
+        put(base, 1, layer.norm1.bias)
+        put(base, 2, att.q_proj.weight, att.k_proj.weight, att.v_proj.weight)
+        put(base, 3, att.q_proj.bias, att.k_proj.bias, att.v_proj.bias)
+        put(base, 4, att.out_proj.weight)
+        put(base, 5, att.out_proj.bias)
+        put(base, 6, layer.norm2.weight)
+        put(base, 7, layer.norm2.bias)
+        put(base, 8, layer.ffn_in.weight)
+        put(base, 9, layer.ffn_in.bias)
+        put(base, 10, layer.ffn_out.weight)
+        put(base, 11, layer.ffn_out.bias)
+    dpad = (d + 63) // 64 * 64
+    packed[final:final + d].copy_(model.final_norm.weight.detach().reshape(-1))
+    packed[final + dpad:final + dpad + d].copy_(model.final_norm.bias.detach().reshape(-1))
+    return packed
+
+
+class OptimizedTransformer(nn.Module):
+    """Inference-only module running the pre-LN stack through the gfx950 HIP library."""
+
+    def __init__(self, parameter_model: nn.Module, plan: int = PLAN_AUTO) -> None:
+        super().__init__()
+        self.parameter_model = parameter_model
+        self.config = parameter_model.config
+        self.plan = plan
+        self.register_buffer("packed_weights", None, persistent=False)
+        self._workspaces: Dict[Tuple[int, int, int], torch.Tensor] = {}
+
+    def prepare(self) -> None:
+        check_supported(self.config)
+        lib = _lib.load()
+        self.packed_weights = pack_model_weights(self.parameter_model)
+        self._lib = lib
+
+    def _workspace(self, batch: int, seq: int, device: torch.device) -> torch.Tensor:
+        key = (batch, seq, device.index if device.index is not None else 0)
+        ws = self._workspaces.get(key)
+        if ws is None:
+            cfg = self.config
+            nbytes = _lib.workspace_bytes(batch, seq, cfg.d_model, cfg.num_heads, cfg.ffn_dim)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            self._workspaces[key] = ws
+        return ws
+
+    def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None):
+        if self.packed_weights is None:
+            self.prepare()
+        cfg = self.config
+        if x.dim() != 3 or x.shape[2] != cfg.d_model:
+            raise ValueError(f"x must be [B, S, {cfg.d_model}], got {tuple(x.shape)}")
+        if x.dtype != torch.float16 or x.device.type != "cuda":
+            raise ValueError("x must be a CUDA float16 tensor")
+        if self.packed_weights.device != x.device or self.packed_weights.dtype != torch.float16:
+            raise ValueError("packed weights and input must be fp16 on the same device")
+        batch, seq, _ = x.shape
+        x = x.contiguous()
+        mask_ptr = None
+        if valid_token_mask is not None:
+            if valid_token_mask.shape != (batch, seq) or valid_token_mask.dtype != torch.bool:
+                raise ValueError("valid_token_mask must be a bool [B, S] tensor")
+            if valid_token_mask.device != x.device:
+                raise ValueError("valid_token_mask must be on the input's device")
+            valid_token_mask = valid_token_mask.contiguous()
+            mask_ptr = valid_token_mask.data_ptr()
+        y = torch.empty_like(x)
+        if batch * seq == 0:
+            return y
+        ws = self._workspace(batch, seq, x.device)
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        rc = self._lib.tt_transformer_fwd(
+            self.packed_weights.data_ptr(), x.data_ptr(), mask_ptr, y.data_ptr(), ws.data_ptr(),
+            ws.numel(), batch, seq, cfg.d_model, cfg.num_heads, cfg.ffn_dim, cfg.num_layers,
+            int(bool(cfg.causal)), self.plan, stream)
+        _lib.check(rc, "tt_transformer_fwd")
+        return y
+
+
+def make_optimized_transformer(parameter_model: nn.Module, *, verbose_build: bool = False,
+                               plan: int = PLAN_AUTO) -> nn.Module:
+    """Build and prepare the optimized module for ``parameter_model``.
+
+    ``parameter_model`` supplies the weights and must already be on its ROCm device in fp16
+    (the reference's contract, optimized_transformer.py:74-77).  ``verbose_build`` is accepted for
+    signature compatibility; the library is prebuilt, so there is nothing to report.
+    """
+    del verbose_build
+    check_supported(parameter_model.config)
+    module = OptimizedTransformer(parameter_model, plan=plan)
+    module.prepare()
+    return module
