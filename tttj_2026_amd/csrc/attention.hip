@@ -99,23 +99,23 @@ __global__ __launch_bounds__(256) void attention_kernel(
     for (int e = 0; e < 16; ++e) o[i][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  uint4 rk[KPT], rv[VPT];
+  u32x4 rk[KPT], rv[VPT];
   auto gload = [&](int t0) {
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int id = tid + 256 * i, r = id / KCH, c = id % KCH, key = t0 + r;
-      rk[i] = key < S ? *(const uint4*)(Kbh + (size_t)key * HD + c * 8) : make_uint4(0, 0, 0, 0);
+      rk[i] = key < S ? *(const u32x4*)(Kbh + (size_t)key * HD + c * 8) : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int id = tid + 256 * i, d = id >> 3, c = id & 7, key = t0 + 8 * c;
-      uint4 v = *(const uint4*)(Vbh + (size_t)d * ldv + key);  // in bounds: rows padded to ldv
+      u32x4 v = *(const u32x4*)(Vbh + (size_t)d * ldv + key);  // in bounds: rows padded to ldv
       if (key + 8 > S) {
         half8 hv = *(half8*)&v;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           if (key + e >= S) hv[e] = (half)0.f;
-        v = *(uint4*)&hv;
+        v = *(u32x4*)&hv;
       }
       rv[i] = v;
     }
@@ -125,12 +125,12 @@ __global__ __launch_bounds__(256) void attention_kernel(
     for (int i = 0; i < KPT; ++i) {
       const int id = tid + 256 * i, r = id / KCH, c = id % KCH;
       const int pos = (r & ~31) | pi23(r & 31);
-      *(uint4*)(&sk[st][pos * HD + kswz<HD>(pos, c) * 8]) = rk[i];
+      *(u32x4*)(&sk[st][pos * HD + kswz<HD>(pos, c) * 8]) = rk[i];
     }
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int id = tid + 256 * i, d = id >> 3, c = id & 7;
-      *(uint4*)(&sv[st][d * kBKV + swz(d, c) * 8]) = rv[i];
+      *(u32x4*)(&sv[st][d * kBKV + swz(d, c) * 8]) = rv[i];
     }
   };
 
@@ -226,7 +226,7 @@ __global__ __launch_bounds__(256) void attention_kernel(
       const int d = 32 * i + 8 * g + 4 * hf;
       half4 v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (half)(o[i][4 * g + e] * inv);
+      for (int e = 0; e < 4; ++e) v[e] = qvalid ? (half)(o[i][4 * g + e] * inv) : (half)0.f;
       *(half4*)(dst + d) = v;
     }
 }

@@ -14,6 +14,9 @@ using half = _Float16;
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+// 16-byte staging register.  A native vector (not the uint4 struct): LLVM turns a struct
+// load + store pair into a memcpy placed at the store, which would delay a prefetch load.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kWave = 64;

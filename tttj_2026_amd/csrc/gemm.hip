@@ -97,41 +97,16 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave % WAVES_N, wm = wave / WAVES_N;
 
-  // Global source pointers of this thread's 16-byte chunks (rows past M are clamped to M-1: they
-  // load valid memory and their results are never stored).
-  const half* xsrc[XCH];
-  const half* wsrc[WCH];
+  // Thread t loads 16-byte chunk (t & 7) of rows (t >> 3) + i * (NT / 8) of both tiles.  Rows
+  // past M are clamped to M-1: they load valid memory and their results are never stored.
+  constexpr int RS = NT / 8;
+  const int c0 = tid & 7, r0 = tid >> 3;
+  const half* xbase = X + c0 * 8;
+  const half* wbase = W + (size_t)(n0 + r0) * K + c0 * 8;
+  int xrow[XCH];
 #pragma unroll
-  for (int i = 0; i < XCH; ++i) {
-    const int id = tid + i * NT, row = id >> 3, c = id & 7;
-    xsrc[i] = X + (size_t)min(m0 + row, M - 1) * K + c * 8;
-  }
-#pragma unroll
-  for (int i = 0; i < WCH; ++i) {
-    const int id = tid + i * NT, row = id >> 3, c = id & 7;
-    wsrc[i] = W + (size_t)(n0 + row) * K + c * 8;
-  }
-  uint4 rx[XCH], rw[WCH];
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < XCH; ++i) rx[i] = *(const uint4*)(xsrc[i] + k0);
-#pragma unroll
-    for (int i = 0; i < WCH; ++i) rw[i] = *(const uint4*)(wsrc[i] + k0);
-  };
-  auto lstore = [&](int st) {
-    half* sx = lds + st * STAGE;
-    half* sw = sx + BM * kBK;
-#pragma unroll
-    for (int i = 0; i < XCH; ++i) {
-      const int id = tid + i * NT, row = id >> 3, c = id & 7;
-      *(uint4*)(sx + row * kBK + swz(row, c) * 8) = rx[i];
-    }
-#pragma unroll
-    for (int i = 0; i < WCH; ++i) {
-      const int id = tid + i * NT, row = id >> 3, c = id & 7;
-      *(uint4*)(sw + row * kBK + swz(row, c) * 8) = rw[i];
-    }
-  };
+  for (int i = 0; i < XCH; ++i) xrow[i] = min(m0 + r0 + i * RS, M - 1);
+  u32x4 rx[XCH], rw[WCH];
 
   floatx16 acc[FN][FM];
 #pragma unroll
@@ -141,37 +116,74 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
+#define TT_GLOAD(k0)                                                                     \
+  do {                                                                                   \
+    _Pragma("unroll") for (int i = 0; i < XCH; ++i)                                      \
+        rx[i] = *(const u32x4*)(xbase + (size_t)xrow[i] * K + (k0));                     \
+    _Pragma("unroll") for (int i = 0; i < WCH; ++i)                                      \
+        rw[i] = *(const u32x4*)(wbase + (size_t)i * RS * K + (k0));                      \
+  } while (0)
+#define TT_LSTORE(st)                                                                    \
+  do {                                                                                   \
+    half* sx_ = lds + (st) * STAGE;                                                      \
+    half* sw_ = sx_ + BM * kBK;                                                          \
+    _Pragma("unroll") for (int i = 0; i < XCH; ++i) {                                    \
+      const int row = r0 + i * RS;                                                       \
+      *(u32x4*)(sx_ + row * kBK + swz(row, c0) * 8) = rx[i];                             \
+    }                                                                                    \
+    _Pragma("unroll") for (int i = 0; i < WCH; ++i) {                                    \
+      const int row = r0 + i * RS;                                                       \
+      *(u32x4*)(sw_ + row * kBK + swz(row, c0) * 8) = rw[i];                             \
+    }                                                                                    \
+  } while (0)
+  // Fragment reads of K step kk+1 are issued before the MFMAs of step kk (two register sets);
+  // scheduling barriers pin that order.
+#define TT_FRAGS(buf, kk, sx, sw)                                                        \
+  do {                                                                                   \
+    const int c_ = 2 * (kk) + (lane >> 5);                                               \
+    _Pragma("unroll") for (int i = 0; i < FN; ++i) {                                     \
+      const int row = wn * WN + i * 32 + (lane & 31);                                    \
+      af[buf][i] = *(const half8*)((sw) + row * kBK + swz(row, c_) * 8);                 \
+    }                                                                                    \
+    _Pragma("unroll") for (int j = 0; j < FM; ++j) {                                     \
+      const int row = wm * WM + j * 32 + (lane & 31);                                    \
+      bf[buf][j] = *(const half8*)((sx) + row * kBK + swz(row, c_) * 8);                 \
+    }                                                                                    \
+  } while (0)
+#define TT_COMPUTE(st)                                                                   \
+  do {                                                                                   \
+    const half* sx_ = lds + (st) * STAGE;                                                \
+    const half* sw_ = sx_ + BM * kBK;                                                    \
+    half8 af[2][FN], bf[2][FM];                                                          \
+    TT_FRAGS(0, 0, sx_, sw_);                                                            \
+    _Pragma("unroll") for (int kk = 0; kk < kBK / 16; ++kk) {                            \
+      if (kk + 1 < kBK / 16) TT_FRAGS((kk + 1) & 1, kk + 1, sx_, sw_);                   \
+      __builtin_amdgcn_sched_barrier(0);                                                 \
+      _Pragma("unroll") for (int i = 0; i < FN; ++i)                                     \
+          _Pragma("unroll") for (int j = 0; j < FM; ++j) acc[i][j] =                     \
+              mfma32x32x16(af[kk & 1][i], bf[kk & 1][j], acc[i][j]);                     \
+      __builtin_amdgcn_sched_barrier(0);                                                 \
+    }                                                                                    \
+  } while (0)
+
+  // Main loop: the last K step is peeled so the body has no conditional (a conditional
+  // prefetch makes the compiler spill the prefetch registers and wait on the loads at once).
   const int nk = K / kBK;
-  gload(0);
-  lstore(0);
+  TT_GLOAD(0);
+  TT_LSTORE(0);
   __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int st = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * kBK);
-    const half* sx = lds + st * STAGE;
-    const half* sw = sx + BM * kBK;
-#pragma unroll
-    for (int kk = 0; kk < kBK / 16; ++kk) {
-      const int c = 2 * kk + (lane >> 5);
-      half8 af[FN], bf[FM];
-#pragma unroll
-      for (int i = 0; i < FN; ++i) {
-        const int row = wn * WN + i * 32 + (lane & 31);
-        af[i] = *(const half8*)(sw + row * kBK + swz(row, c) * 8);
-      }
-#pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        const int row = wm * WM + j * 32 + (lane & 31);
-        bf[j] = *(const half8*)(sx + row * kBK + swz(row, c) * 8);
-      }
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-#pragma unroll
-        for (int j = 0; j < FM; ++j) acc[i][j] = mfma32x32x16(af[i], bf[j], acc[i][j]);
-    }
-    if (kt + 1 < nk) lstore(st ^ 1);
+  for (int kt = 0; kt < nk - 1; ++kt) {
+    TT_GLOAD((kt + 1) * kBK);
+    __builtin_amdgcn_sched_barrier(0);
+    TT_COMPUTE(kt & 1);
+    TT_LSTORE((kt + 1) & 1);
     __syncthreads();
   }
+  TT_COMPUTE((nk - 1) & 1);
+#undef TT_FRAGS
+#undef TT_COMPUTE
+#undef TT_GLOAD
+#undef TT_LSTORE
 
   // Epilogue: acc[i][j][4g+e] = C[m][n] with m = row j*32 + lane%32 of the wave tile and
   // n = i*32 + 8g + 4*(lane/32) + e.
