@@ -163,6 +163,31 @@ def kernel_breakdown(name, dev, iters=20):
     return res
 
 
+COPY_ELEMS = 64 * 1024 * 1024  # fp16 elements: 128 MiB read + 128 MiB written per copy
+
+
+def copy_calibration(dev, reps=3):
+    """A plain device copy of known size; its FETCH_SIZE / WRITE_SIZE counters calibrate the
+    counters read for the kernels (bytes per dispatch = 128 MiB each way)."""
+    a = torch.ones(COPY_ELEMS, dtype=torch.float16, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+
+
+def load_traffic(name, kernel):
+    """HBM bytes per launch of ``kernel`` at ``name`` from the committed rocprofv3 counter
+    summary (profiles/traffic.json), or None when no counter run covers it."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            table = json.load(f)
+        return table[name][kernel]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError, TypeError):
+        return None
+
+
 def cpu_baseline(name, budget_s, gpu_out=None):
     """Time the fp32 CPU oracle (this repo's restatement of BaselineTransformer) on host cores."""
     from oracle import transformer_oracle as O
@@ -226,6 +251,9 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU oracle work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-eager", action="store_true")
+    ap.add_argument("--mode", default="full", choices=("full", "kernels"),
+                    help="kernels: only run each kernel of one layer (and a copy of known size) "
+                         "a few times, for rocprofv3 counter runs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -238,6 +266,11 @@ def main() -> int:
     dev = torch.device("cuda:0")
     name = args.workload
     cfg = WORKLOADS[name].config
+    if args.mode == "kernels":
+        copy_calibration(dev)
+        res = kernel_breakdown(name, dev, iters=args.steps)
+        print(json.dumps({"workload": name, "kernels": res}))
+        return 0
 
     head, (model, opt, xd, md, x16, mask) = bench_workload(
         name, args.steps, args.warmup, args.rounds, not args.no_eager, dev)
@@ -255,11 +288,13 @@ def main() -> int:
     dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["ms_per_forward"])
     if dom["bound"] == "mfma":
         rl = {"kernel": dom_name, "bound": "mfma", "achieved": dom["achieved_tflops"],
-              "peak": PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"], "traffic": None,
+              "peak": PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"],
+              "traffic": load_traffic(name, dom_name),
               "work_per_launch": dom["flops"], "avg_launch_ms": dom["avg_ms"]}
     else:
         rl = {"kernel": dom_name, "bound": "hbm", "achieved": dom["achieved_gbps"],
-              "peak": PEAK_GBPS, "unit": "GB/s", "frac": dom["frac"], "traffic": None,
+              "peak": PEAK_GBPS, "unit": "GB/s", "frac": dom["frac"],
+              "traffic": load_traffic(name, dom_name),
               "work_per_launch": dom["bytes"], "avg_launch_ms": dom["avg_ms"]}
 
     per_config = {}

@@ -230,3 +230,32 @@ def test_mask_info(device):
     assert info == [3, 3, 0, 5, 1, 0, 1, 1]
     info = ops.mask_info(None, 2, 7, device).cpu().tolist()
     assert info == [7, 7, 1, 1]
+
+
+def test_gelu_epilogue_matches_exact_erf_gelu(device):
+    """GELU epilogue on every fp16 pre-activation in [-12, 12]: the GEMM is arranged so that the
+    accumulator equals the value exactly (x = [v, 0, ...], every weight row = e_0, bias 0), and the
+    fp16 output must equal the correctly rounded exact-erf GELU (float64 math.erf) up to one fp16
+    ulp, with at most 0.1% of values off by that ulp (values within ~1e-7 of a rounding tie)."""
+    vals = torch.arange(-(2 ** 15), 2 ** 15, dtype=torch.int32).to(torch.int16).view(torch.float16)
+    vals = vals[torch.isfinite(vals) & (vals.float().abs() <= 12)]
+    m, n, k = vals.numel(), 64, 64
+    x = torch.zeros(m, k, dtype=torch.float16)
+    x[:, 0] = vals
+    w = torch.zeros(n, k, dtype=torch.float16)
+    w[:, 0] = 1
+    y = ops.linear(x.to(device), w.to(device), torch.zeros(n, dtype=torch.float16, device=device),
+                   "gelu")
+    torch.cuda.synchronize()
+    got = y[:, 0].cpu()
+    assert (y.cpu() == got[:, None]).all()           # every output column is the same function
+    v64 = vals.double()
+    exact = 0.5 * v64 * (1.0 + torch.erf(v64 / math.sqrt(2.0)))
+    want = exact.half()
+    ulp = (got.view(torch.int16).int() - want.view(torch.int16).int()).abs()
+    ulp = torch.where((got == 0) & (want == 0), torch.zeros_like(ulp), ulp)  # +0 vs -0
+    assert ulp.max().item() <= 1
+    assert (ulp > 0).float().mean().item() < 1e-3
+    err = (got.double() - exact).abs()
+    half_ulp = (want.double().abs().clamp_min(2 ** -14) * 2 ** -11)
+    assert (err <= half_ulp + 1e-6).all()

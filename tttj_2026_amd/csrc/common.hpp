@@ -63,8 +63,26 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 __device__ __forceinline__ float gelu_erf(float v) {
-  // Exact GELU, F.gelu(approximate="none"): 0.5 v (1 + erf(v / sqrt 2)).
-  return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+  // Exact-erf GELU, F.gelu(approximate="none"): v * Phi(v), Phi(v) = erfc(-v / sqrt 2) / 2.
+  // erfc(z), z = |v| / sqrt 2, is t * exp(-z^2 + P(t)) with t = 1 / (1 + z/2) and P a degree-9
+  // polynomial fitted at Chebyshev nodes (the form of Numerical Recipes 6.2; coefficients derived
+  // by fit_erfc.py), relative error < 1e-7 for all z.  Phi(v) = 1 - q for v >= 0 and q for v < 0
+  // with q = erfc(z) / 2, so the result is branch-free and keeps full relative accuracy in the
+  // negative tail: the fp16 result is the correctly rounded GELU except within ~1e-7 of a tie.
+  const float z = fabsf(v) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
+  float p = 1.784814059e-01f;
+  p = fmaf(p, t, -8.587818905e-01f);
+  p = fmaf(p, t, 1.562995793e+00f);
+  p = fmaf(p, t, -1.218379551e+00f);
+  p = fmaf(p, t, 3.344113965e-01f);
+  p = fmaf(p, t, -2.089165053e-01f);
+  p = fmaf(p, t, 1.022820283e-01f);
+  p = fmaf(p, t, 3.733488146e-01f);
+  p = fmaf(p, t, 1.000071867e+00f);
+  p = fmaf(p, t, -1.265513274e+00f);
+  const float q = 0.5f * t * __builtin_amdgcn_exp2f((p - z * z) * 1.4426950408889634f);
+  return v * (v >= 0.f ? 1.0f - q : q);
 }
 
 // 16-byte element chunk index swizzle for [rows][64 halfs] LDS tiles (128-byte rows): XOR with the

@@ -4,11 +4,14 @@
 // Design (gfx950):
 //  * Both operands are K-contiguous (nn.Linear weights are [N,K]), so a block stages a BM x 64
 //    X tile and a BN x 64 W tile in LDS per K step (128-byte rows, 16-byte chunks XOR-swizzled
-//    by row so ds_read_b128 fragment reads are bank-conflict free), double-buffered, with the
-//    next K step's global loads issued into registers before the current step's MFMAs.
+//    by row so ds_read_b128 fragment reads are bank-conflict free), double-buffered.  The copies
+//    are global_load_lds_dwordx4 (global -> LDS without a register round trip), issued for the
+//    next K step during the first half of the current one, one between consecutive MFMAs, with
+//    the next k-step's fragment reads interleaved the same way (sched_group_barrier).
 //  * The MFMA is v_mfma_f32_32x32x16_f16 with W as the "A" operand and X as "B", i.e. each wave
-//    accumulates C^T: lane l then holds 4 consecutive output features of one token per group,
-//    so the epilogue writes 8-byte runs of a row of Y and reads bias / residual the same way.
+//    accumulates C^T: lane l then holds 4 consecutive output features of one token per group.
+//    The epilogue (bias, GELU, residual, row mask, QKV head-major scatter) stages each wave's
+//    tile through LDS and writes whole rows with 16-byte stores.
 //  * Block-id -> tile mapping is XCD-aware: workgroup i runs on XCD i % 8, so each XCD is given
 //    a contiguous range of tile ids, and tiles are ordered in groups of 8 row-tiles so the tiles
 //    one XCD runs at once share X row panels and W column panels in that XCD's L2.
@@ -16,6 +19,7 @@
 #include "kernels.hpp"
 
 #include <mutex>
+#include <type_traits>
 
 namespace tt {
 
@@ -36,56 +40,48 @@ __device__ __forceinline__ void tile_coords(int t, int tiles_m, int tiles_n, int
   tn = r / gm;
 }
 
-// Apply the epilogue to 4 consecutive output features n..n+3 of row m.
-__device__ __forceinline__ void epilogue4(const EpiArgs& ep, int m, int n, float v0, float v1,
-                                          float v2, float v3) {
-  const half4 b = *(const half4*)(ep.bias + n);
-  float v[4] = {v0 + (float)b[0], v1 + (float)b[1], v2 + (float)b[2], v3 + (float)b[3]};
-  const int mode = ep.mode;
-  if (mode == TT_EPI_BIAS_GELU) {
+// Scalar store of 4 consecutive output features n..n+3 of row m into the QKV layout (used only
+// for the V^T part when tokens of one 8-row group may belong to two sequences, S % 8 != 0).
+__device__ __forceinline__ void store_vt4(const EpiArgs& ep, int m, int n, half4 h) {
+  const int D = ep.d_model, hd = ep.head_dim, S = ep.seq;
+  const int nn = n - 2 * D;
+  const int hh = nn / hd, d = nn - hh * hd;
+  const int bb = m / S, s = m - bb * S;
+  const size_t plane = (size_t)ep.batch * S * D;
+  const size_t ldv = (size_t)(S + 63) / 64 * 64;
+  half* vt = ep.y + 2 * plane + (((size_t)bb * ep.heads + hh) * hd + d) * ldv + s;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
-  } else if (mode == TT_EPI_RESID_MASKED || mode == TT_EPI_MASKED_RESID) {
-    const bool ok = ep.valid == nullptr || ep.valid[m] != 0;
-    const half4 r = *(const half4*)(ep.resid + (size_t)m * ep.ldy + n);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (mode == TT_EPI_RESID_MASKED)
-        v[e] = (float)r[e] + (ok ? v[e] : 0.f);
-      else
-        v[e] = ok ? (float)r[e] + v[e] : 0.f;
-    }
-  } else if (mode == TT_EPI_QKV) {
-    const int D = ep.d_model, hd = ep.head_dim, S = ep.seq;
-    const int which = n / D, nn = n - which * D;
-    const int h = nn / hd, d = nn - h * hd;
-    const int bb = m / S, s = m - bb * S;
-    const size_t plane = (size_t)ep.batch * S * D;
-    const size_t bh = (size_t)bb * ep.heads + h;
-    if (which < 2) {
-      half4 o = {(half)v[0], (half)v[1], (half)v[2], (half)v[3]};
-      *(half4*)(ep.y + which * plane + (bh * S + s) * hd + d) = o;
-    } else {
-      const size_t ldv = (size_t)(S + 63) / 64 * 64;  // V^T rows padded to a multiple of 64 keys
-      half* vt = ep.y + 2 * plane + (bh * hd + d) * ldv + s;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) vt[(size_t)e * ldv] = (half)v[e];
-    }
-    return;
-  }
-  half4 o = {(half)v[0], (half)v[1], (half)v[2], (half)v[3]};
-  *(half4*)(ep.y + (size_t)m * ep.ldy + n) = o;
+  for (int e = 0; e < 4; ++e) vt[(size_t)e * ldv] = h[e];
 }
 
-template <int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_kernel(
-    const half* __restrict__ X, const half* __restrict__ W, int M, int N, int K, EpiArgs ep) {
-  constexpr int WAVES_N = BN / WN;
-  constexpr int NT = (BM / WM) * WAVES_N * 64;
-  constexpr int FN = WN / 32, FM = WM / 32;
-  constexpr int XCH = BM * 8 / NT, WCH = BN * 8 / NT;
-  static_assert(XCH * NT == BM * 8 && WCH * NT == BN * 8, "tile/thread mismatch");
-  constexpr int STAGE = (BM + BN) * kBK;
+__device__ __forceinline__ half8 swap_halves(half8 t) {
+  return half8{t[4], t[5], t[6], t[7], t[0], t[1], t[2], t[3]};
+}
+
+// LDS tile of R rows x 64 halfs (128-byte rows) holding a K slice of one operand.  Global ->
+// LDS copies use global_load_lds_dwordx4: one instruction moves 1 KiB, lane l writing LDS bytes
+// [16 l, 16 l + 16) of an 8-row group, i.e. row l / 8, physical chunk l % 8.  The chunk swizzle is
+// applied on the global side: lane l fetches logical chunk (l % 8) ^ (l / 8) of its row, so the
+// physical chunk of logical chunk c in row r is c ^ (r % 8), as swz() expects.
+__device__ __forceinline__ void lds_copy16(const half* src, half* lds_dst) {
+  __builtin_amdgcn_global_load_lds((const void*)src,
+                                   (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
+}
+
+template <int BM, int BN, int MODE>
+__global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
+                                                   const half* __restrict__ W, int M, int N, int K,
+                                                   EpiArgs ep) {
+  // 2 x 2 waves, each owning a (BM/2) x (BN/2) block of C as FM x FN 32x32 MFMA tiles.
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int FM = WM / 32, FN = WN / 32;
+  constexpr int ROWS = BM + BN;       // LDS rows per stage: X rows [0, BM), W rows [BM, BM + BN)
+  constexpr int STAGE = ROWS * kBK;   // halfs per stage
+  constexpr int XL = BM / 32;         // X copies per wave per stage (8 rows x 4 waves each)
+  constexpr int WL = BN / 32;         // W copies per wave per stage
+  constexpr int NL = XL + WL;
+  constexpr int KSUB = kBK / 16;      // MFMA k-steps per stage
+  constexpr int CSPREAD = KSUB / 2;
 
   extern __shared__ __align__(16) half lds[];
 
@@ -94,19 +90,23 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_kernel(
   tile_coords(xcd_remap(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wn = wave % WAVES_N, wm = wave / WAVES_N;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wn = wave & 1, wm = wave >> 1;
 
-  // Thread t loads 16-byte chunk (t & 7) of rows (t >> 3) + i * (NT / 8) of both tiles.  Rows
-  // past M are clamped to M-1: they load valid memory and their results are never stored.
-  constexpr int RS = NT / 8;
-  const int c0 = tid & 7, r0 = tid >> 3;
-  const half* xbase = X + c0 * 8;
-  const half* wbase = W + (size_t)(n0 + r0) * K + c0 * 8;
-  int xrow[XCH];
+  // Copy sources: copy i of this wave fills 8-row group wave + 4 i of the stage.  X rows past M
+  // are clamped to M - 1 (valid memory whose results are never stored).
+  const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
+  int src_off[NL];
 #pragma unroll
-  for (int i = 0; i < XCH; ++i) xrow[i] = min(m0 + r0 + i * RS, M - 1);
-  u32x4 rx[XCH], rw[WCH];
+  for (int i = 0; i < NL; ++i) {
+    const int r = (wave + 4 * i) * 8 + lrow;
+    if (i < XL) src_off[i] = min(m0 + r, M - 1) * K + lchunk * 8;
+    else src_off[i] = (n0 + r - BM) * K + lchunk * 8;
+  }
+  auto copy = [&](int i, int k0, half* stage) {
+    const half* base = (i < XL) ? X : W;
+    lds_copy16(base + src_off[i] + k0, stage + (wave + 4 * i) * 8 * kBK);
+  };
 
   floatx16 acc[FN][FM];
 #pragma unroll
@@ -116,89 +116,199 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-#define TT_GLOAD(k0)                                                                     \
-  do {                                                                                   \
-    _Pragma("unroll") for (int i = 0; i < XCH; ++i)                                      \
-        rx[i] = *(const u32x4*)(xbase + (size_t)xrow[i] * K + (k0));                     \
-    _Pragma("unroll") for (int i = 0; i < WCH; ++i)                                      \
-        rw[i] = *(const u32x4*)(wbase + (size_t)i * RS * K + (k0));                      \
-  } while (0)
-#define TT_LSTORE(st)                                                                    \
-  do {                                                                                   \
-    half* sx_ = lds + (st) * STAGE;                                                      \
-    half* sw_ = sx_ + BM * kBK;                                                          \
-    _Pragma("unroll") for (int i = 0; i < XCH; ++i) {                                    \
-      const int row = r0 + i * RS;                                                       \
-      *(u32x4*)(sx_ + row * kBK + swz(row, c0) * 8) = rx[i];                             \
-    }                                                                                    \
-    _Pragma("unroll") for (int i = 0; i < WCH; ++i) {                                    \
-      const int row = r0 + i * RS;                                                       \
-      *(u32x4*)(sw_ + row * kBK + swz(row, c0) * 8) = rw[i];                             \
-    }                                                                                    \
-  } while (0)
-  // Fragment reads of K step kk+1 are issued before the MFMAs of step kk (two register sets);
-  // scheduling barriers pin that order.
-#define TT_FRAGS(buf, kk, sx, sw)                                                        \
-  do {                                                                                   \
-    const int c_ = 2 * (kk) + (lane >> 5);                                               \
-    _Pragma("unroll") for (int i = 0; i < FN; ++i) {                                     \
-      const int row = wn * WN + i * 32 + (lane & 31);                                    \
-      af[buf][i] = *(const half8*)((sw) + row * kBK + swz(row, c_) * 8);                 \
-    }                                                                                    \
-    _Pragma("unroll") for (int j = 0; j < FM; ++j) {                                     \
-      const int row = wm * WM + j * 32 + (lane & 31);                                    \
-      bf[buf][j] = *(const half8*)((sx) + row * kBK + swz(row, c_) * 8);                 \
-    }                                                                                    \
-  } while (0)
-#define TT_COMPUTE(st)                                                                   \
-  do {                                                                                   \
-    const half* sx_ = lds + (st) * STAGE;                                                \
-    const half* sw_ = sx_ + BM * kBK;                                                    \
-    half8 af[2][FN], bf[2][FM];                                                          \
-    TT_FRAGS(0, 0, sx_, sw_);                                                            \
-    _Pragma("unroll") for (int kk = 0; kk < kBK / 16; ++kk) {                            \
-      if (kk + 1 < kBK / 16) TT_FRAGS((kk + 1) & 1, kk + 1, sx_, sw_);                   \
-      __builtin_amdgcn_sched_barrier(0);                                                 \
-      _Pragma("unroll") for (int i = 0; i < FN; ++i)                                     \
-          _Pragma("unroll") for (int j = 0; j < FM; ++j) acc[i][j] =                     \
-              mfma32x32x16(af[kk & 1][i], bf[kk & 1][j], acc[i][j]);                     \
-      __builtin_amdgcn_sched_barrier(0);                                                 \
-    }                                                                                    \
-  } while (0)
+  // The block's bias slice goes to LDS once (made visible by the prologue's barrier).
+  __shared__ __align__(16) half sbias[BN];
+  if (threadIdx.x < BN / 8)
+    *(u32x4*)(sbias + 8 * threadIdx.x) = *(const u32x4*)(ep.bias + n0 + 8 * threadIdx.x);
 
-  // Main loop: the last K step is peeled so the body has no conditional (a conditional
-  // prefetch makes the compiler spill the prefetch registers and wait on the loads at once).
+  // Fragment addressing: A = W rows (output features), B = X rows (tokens); lane l reads row
+  // l % 32 of a 32-row block at logical chunk 2 kk + l / 32, physically XOR (l % 8).
+  const int frow = lane & 31, fhi = lane >> 5, fx = lane & 7;
+  half8 af[2][FN], bf[2][FM];
+  auto frags = [&](int buf, int kk, const half* stage) {
+    const int pc = (2 * kk + fhi) ^ fx;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+      af[buf][i] = *(const half8*)(stage + (BM + wn * WN + i * 32 + frow) * kBK + pc * 8);
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+      bf[buf][j] = *(const half8*)(stage + (wm * WM + j * 32 + frow) * kBK + pc * 8);
+  };
+
+  // One stage: KSUB k-steps of FN x FM MFMAs.  Fragment reads for k-step kk + 1 and (MORE) the
+  // copies of the next stage are interleaved one per MFMA.
+  auto stage = [&](auto more_tag, const half* cur, half* nxt, int k1) {
+    constexpr bool MORE = decltype(more_tag)::value;
+    frags(0, 0, cur);
+#pragma unroll
+    for (int kk = 0; kk < KSUB; ++kk) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (kk + 1 < KSUB) frags((kk + 1) & 1, kk + 1, cur);
+      // The next stage's copies go out during the first CSPREAD k-steps, so they have most of
+      // the stage to land before the end-of-stage wait.
+      const int c_lo = kk < CSPREAD ? kk * NL / CSPREAD : NL;
+      const int c_hi = kk < CSPREAD ? (kk + 1) * NL / CSPREAD : NL;
+      if constexpr (MORE) {
+#pragma unroll
+        for (int c = c_lo; c < c_hi; ++c) copy(c, k1, nxt);
+      }
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          acc[i][j] = mfma32x32x16(af[kk & 1][i], bf[kk & 1][j], acc[i][j]);
+      if (kk + 1 < KSUB) {
+#pragma unroll
+        for (int t = 0; t < FN + FM; ++t) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+      }
+      if constexpr (MORE) {
+#pragma unroll
+        for (int c = c_lo; c < c_hi; ++c) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, FN * FM, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
   const int nk = K / kBK;
-  TT_GLOAD(0);
-  TT_LSTORE(0);
+  // Prologue: stage 0.
+#pragma unroll
+  for (int i = 0; i < NL; ++i) copy(i, 0, lds);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int kt = 0; kt < nk - 1; ++kt) {
-    TT_GLOAD((kt + 1) * kBK);
-    __builtin_amdgcn_sched_barrier(0);
-    TT_COMPUTE(kt & 1);
-    TT_LSTORE((kt + 1) & 1);
+    stage(std::true_type{}, lds + (kt & 1) * STAGE, lds + ((kt + 1) & 1) * STAGE, (kt + 1) * kBK);
+    // The next stage's copies have landed in LDS and every wave is done reading this stage.
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  TT_COMPUTE((nk - 1) & 1);
-#undef TT_FRAGS
-#undef TT_COMPUTE
-#undef TT_GLOAD
-#undef TT_LSTORE
+  stage(std::false_type{}, lds + ((nk - 1) & 1) * STAGE, nullptr, 0);
 
-  // Epilogue: acc[i][j][4g+e] = C[m][n] with m = row j*32 + lane%32 of the wave tile and
-  // n = i*32 + 8g + 4*(lane/32) + e.
+  // ---- Epilogue ----
+  // acc[i][j][4g+e] = C[m][n] with m = row j*32 + lane%32 of the wave tile and
+  // n = i*32 + 8g + 4*(lane/32) + e.  Each wave stages its WM x WN tile of fp16(acc + bias
+  // [, GELU]) in its own LDS area and then writes whole rows with 16-byte stores (residual and
+  // mask applied on the way out), so every store instruction writes full 128-byte lines.
+  // Row-major staging is swizzled in 8-byte units: unit u of row r lives at u ^ (r & SWM), which
+  // keeps the 8-byte writes of 32 consecutive rows and the 16-byte row reads conflict-free.  The
+  // V part of the QKV projection is staged transposed ([n][m]) and written as V^T rows.
+  __syncthreads();  // every wave is done with the last stage's fragments
+  half* cst = lds + wave * (WM * WN);
+  constexpr int UNITS = WN / 4;
+  constexpr int SWM = (UNITS >= 16 ? 16 : UNITS) - 1;
+  const int mw = m0 + wm * WM, nw = n0 + wn * WN;  // wave tile origin
+  bool vt_mode = false, vt_scalar = false;
+  if constexpr (MODE == TT_EPI_QKV) {
+    vt_mode = n0 >= 2 * ep.d_model;   // tiles never straddle the Q / K / V boundaries
+    vt_scalar = vt_mode && (ep.seq % 8 != 0);
+  }
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
-    const int m = m0 + wm * WM + j * 32 + (lane & 31);
-    if (m >= M) continue;
+    const int ml = j * 32 + (lane & 31);
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int n = n0 + wn * WN + i * 32 + 8 * g + 4 * (lane >> 5);
-        epilogue4(ep, m, n, acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                  acc[i][j][4 * g + 3]);
+        const int nl = i * 32 + 8 * g + 4 * (lane >> 5);
+        const half4 bv = *(const half4*)(sbias + wn * WN + nl);
+        half4 h;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = acc[i][j][4 * g + e] + (float)bv[e];
+          if constexpr (MODE == TT_EPI_BIAS_GELU) v = gelu_erf(v);
+          h[e] = (half)v;
+        }
+        if (vt_scalar) {
+          if (mw + ml < M) store_vt4(ep, mw + ml, nw + nl, h);
+        } else if (vt_mode) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) cst[(nl + e) * WM + ml] = h[e];
+        } else {
+          const int u = nl >> 2;
+          *(half4*)(cst + ml * WN + ((u ^ (ml & SWM)) << 2)) = h;
+        }
       }
+    }
+  }
+  if (vt_scalar) return;
+  __builtin_amdgcn_s_waitcnt(0);  // wave-local staging: the LDS writes above precede the reads
+
+  if (vt_mode) {
+    // V^T rows: staged row nl holds WM consecutive tokens of feature nw + nl.  S % 8 == 0 here,
+    // so an aligned group of 8 tokens lies in one sequence and M is a multiple of 8.
+    constexpr int CPR = WM / 8, RPI = 64 / CPR;
+    const int D = ep.d_model, hd = ep.head_dim, S = ep.seq;
+    const size_t plane = (size_t)ep.batch * S * D;
+    const size_t ldv = (size_t)(S + 63) / 64 * 64;
+#pragma unroll 4
+    for (int it = 0; it < WN / RPI; ++it) {
+      const int r = it * RPI + lane / CPR, c = lane % CPR;
+      const int m = mw + 8 * c;
+      if (m >= M) continue;
+      const half8 t = *(const half8*)(cst + r * WM + 8 * c);
+      const int nn = nw + r - 2 * D;
+      const int hh = nn / hd, d = nn - hh * hd;
+      const int bb = m / S, sq = m - bb * S;
+      *(half8*)(ep.y + 2 * plane + (((size_t)bb * ep.heads + hh) * hd + d) * ldv + sq) = t;
+    }
+    return;
+  }
+
+  // Row-major tile: CPR 16-byte chunks per row, RPI rows per wave instruction, processed in
+  // batches of NB instructions whose residual / mask loads are all issued before any store.
+  constexpr int CPR = WN / 8, RPI = 64 / CPR, NIT = WM / RPI;
+  constexpr int NB = NIT < 8 ? NIT : 8;
+  constexpr bool RESID = MODE == TT_EPI_RESID_MASKED || MODE == TT_EPI_MASKED_RESID;
+  const int c = lane % CPR;
+#pragma unroll
+  for (int b0 = 0; b0 < NIT; b0 += NB) {
+    half8 rv[NB];
+    bool ok[NB];
+    if constexpr (RESID) {
+#pragma unroll
+      for (int q = 0; q < NB; ++q) {
+        const int m = min(mw + (b0 + q) * RPI + lane / CPR, M - 1);
+        ok[q] = ep.valid == nullptr || ep.valid[m] != 0;
+        rv[q] = *(const half8*)(ep.resid + (size_t)m * ep.ldy + nw + 8 * c);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const int r = (b0 + q) * RPI + lane / CPR;
+      const int m = mw + r;
+      const int sw = r & SWM;
+      half8 t = *(const half8*)(cst + r * WN + (((2 * c) ^ (sw & ~1)) << 2));
+      if (sw & 1) t = swap_halves(t);
+      if (m >= M) continue;
+      if constexpr (RESID) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if constexpr (MODE == TT_EPI_RESID_MASKED)
+            t[e] = ok[q] ? (half)((float)rv[q][e] + (float)t[e]) : rv[q][e];
+          else
+            t[e] = ok[q] ? (half)((float)rv[q][e] + (float)t[e]) : (half)0.f;
+        }
+      }
+      half* dst;
+      if constexpr (MODE == TT_EPI_QKV) {
+        // Q or K: 8 features of one head of token m -> [B, H, S, hd] row
+        const int D = ep.d_model, hd = ep.head_dim, S = ep.seq;
+        const int n = nw + 8 * c;
+        const int which = n / D, nn = n - which * D;
+        const int hh = nn / hd, d = nn - hh * hd;
+        const int bb = m / S, sq = m - bb * S;
+        dst = ep.y + which * ((size_t)ep.batch * S * D) +
+              (((size_t)bb * ep.heads + hh) * S + sq) * hd + d;
+      } else {
+        dst = ep.y + (size_t)m * ep.ldy + nw + 8 * c;
+      }
+      *(half8*)dst = t;
     }
   }
 }
@@ -206,58 +316,57 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_kernel(
 // ---- host-side tile selection ----
 struct TileCfg {
   int bm, bn;
-  float efficiency;  // relative per-CU MFMA efficiency of the tile shape
 };
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int MODE>
 static int run_tile(const half* x, const half* w, int m, int n, int k, const EpiArgs& ep,
                     hipStream_t stream) {
-  constexpr int NT = (BM / WM) * (BN / WN) * 64;
+  constexpr int NT = 256;
   const size_t lds = 2 * (size_t)(BM + BN) * kBK * sizeof(half);
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
   std::call_once(once, [&] {
-    attr_err = hipFuncSetAttribute((const void*)gemm_kernel<BM, BN, WM, WN>,
+    attr_err = hipFuncSetAttribute((const void*)gemm_kernel<BM, BN, MODE>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   });
   if (attr_err != hipSuccess)
     return fail(TT_ERR_HIP, "hipFuncSetAttribute(gemm %dx%d): %s", BM, BN, hipGetErrorString(attr_err));
   const int tiles = ((m + BM - 1) / BM) * (n / BN);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN>), dim3(tiles), dim3(NT), lds, stream, x, w, m, n,
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, MODE>), dim3(tiles), dim3(NT), lds, stream, x, w, m, n,
                      k, ep);
   return launch_status("gemm_kernel");
 }
 
-static const TileCfg kTiles[] = {
-    {256, 256, 1.00f},
-    {256, 128, 0.92f},
-    {128, 128, 0.80f},
-    {128, 64, 0.65f},
-    {64, 64, 0.50f},
-};
+template <int MODE>
+static int run_mode(int tile, const half* x, const half* w, int m, int n, int k, const EpiArgs& ep,
+                    hipStream_t stream) {
+  switch (tile) {
+    case 0: return run_tile<256, 256, MODE>(x, w, m, n, k, ep, stream);
+    case 1: return run_tile<256, 128, MODE>(x, w, m, n, k, ep, stream);
+    case 2: return run_tile<128, 128, MODE>(x, w, m, n, k, ep, stream);
+    case 3: return run_tile<128, 64, MODE>(x, w, m, n, k, ep, stream);
+    default: return run_tile<64, 64, MODE>(x, w, m, n, k, ep, stream);
+  }
+}
+
+static const TileCfg kTiles[] = {{256, 256}, {256, 128}, {128, 128}, {128, 64}, {64, 64}};
+constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
 static int g_tile_override = -1;  // test hook: force one tile configuration
 
-// Estimated time ~ (tiles per CU, rounded up) x (tile work / relative efficiency): co-resident
-// blocks on one CU share its MFMA throughput, so a CU finishing k blocks costs about k blocks.
-static int pick_tile(int m, int n, int cus) {
-  const int count = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
-  if (g_tile_override >= 0 && g_tile_override < count && n % kTiles[g_tile_override].bn == 0)
+// Tile choice, from measurements on MI355X (M = 8192, N in {1024, 3072, 4096}, K in {1024,
+// 4096, 8192}): a 256x256 block (one per CU, 128 KiB of LDS) only pays off once K is long enough
+// to amortise its prologue and its 128 KiB epilogue (K >= 4096) and the grid still fills every CU;
+// otherwise 128x128 (two blocks per CU, so one block's epilogue overlaps the other's MFMAs) is
+// the fastest shape.  Narrower tiles are used when a wider one would leave CUs idle.
+static int pick_tile(int m, int n, int k, int cus) {
+  if (g_tile_override >= 0 && g_tile_override < kNumTiles && n % kTiles[g_tile_override].bn == 0)
     return g_tile_override;
-  int best = -1;
-  double best_cost = 0;
-  for (int i = 0; i < count; ++i) {
-    const TileCfg& t = kTiles[i];
-    if (n % t.bn != 0) continue;
-    const long tiles = (long)((m + t.bm - 1) / t.bm) * (n / t.bn);
-    const long per_cu = (tiles + cus - 1) / cus;
-    const double cost = (double)per_cu * t.bm * t.bn / t.efficiency;
-    if (best < 0 || cost < best_cost * 0.999) {
-      best = i;
-      best_cost = cost;
-    }
-  }
-  return best;
+  auto tiles = [&](int i) { return (long)((m + kTiles[i].bm - 1) / kTiles[i].bm) * (n / kTiles[i].bn); };
+  if (k >= 4096 && n % 256 == 0 && tiles(0) >= cus) return 0;
+  for (int i = 2; i < kNumTiles; ++i)
+    if (n % kTiles[i].bn == 0 && tiles(i) >= cus) return i;
+  return kNumTiles - 1;  // 64x64: every N that is a multiple of 64
 }
 
 static int device_cus() {
@@ -277,6 +386,8 @@ int launch_linear(const half* x, const half* w, int m, int n, int k, const EpiAr
   TT_REQUIRE(m >= 0 && n > 0 && k > 0, "linear: bad shape m=%d n=%d k=%d", m, n, k);
   TT_REQUIRE(k % kBK == 0, "linear: K=%d must be a multiple of %d", k, kBK);
   TT_REQUIRE(n % 64 == 0, "linear: N=%d must be a multiple of 64", n);
+  TT_REQUIRE((int64_t)m * k < (1LL << 31) && (int64_t)n * k < (1LL << 31),
+             "linear: operands of more than 2^31 elements (m=%d n=%d k=%d)", m, n, k);
   TT_REQUIRE(ep.mode >= TT_EPI_BIAS && ep.mode <= TT_EPI_QKV, "linear: bad epilogue %d", ep.mode);
   TT_REQUIRE(ep.bias != nullptr && ep.y != nullptr, "linear: null bias/output");
   if (ep.mode == TT_EPI_RESID_MASKED || ep.mode == TT_EPI_MASKED_RESID)
@@ -289,20 +400,21 @@ int launch_linear(const half* x, const half* w, int m, int n, int k, const EpiAr
                ep.batch, ep.seq, ep.heads, ep.head_dim);
   }
   if (m == 0) return TT_OK;
-  switch (pick_tile(m, n, device_cus())) {
-    case 0: return run_tile<256, 256, 128, 128>(x, w, m, n, k, ep, stream);
-    case 1: return run_tile<256, 128, 128, 64>(x, w, m, n, k, ep, stream);
-    case 2: return run_tile<128, 128, 64, 64>(x, w, m, n, k, ep, stream);
-    case 3: return run_tile<128, 64, 64, 32>(x, w, m, n, k, ep, stream);
-    default: return run_tile<64, 64, 32, 32>(x, w, m, n, k, ep, stream);
+  const int tile = pick_tile(m, n, k, device_cus());
+  switch (ep.mode) {
+    case TT_EPI_BIAS: return run_mode<TT_EPI_BIAS>(tile, x, w, m, n, k, ep, stream);
+    case TT_EPI_BIAS_GELU: return run_mode<TT_EPI_BIAS_GELU>(tile, x, w, m, n, k, ep, stream);
+    case TT_EPI_RESID_MASKED: return run_mode<TT_EPI_RESID_MASKED>(tile, x, w, m, n, k, ep, stream);
+    case TT_EPI_MASKED_RESID: return run_mode<TT_EPI_MASKED_RESID>(tile, x, w, m, n, k, ep, stream);
+    default: return run_mode<TT_EPI_QKV>(tile, x, w, m, n, k, ep, stream);
   }
 }
 
 }  // namespace tt
 
 extern "C" int tt_gemm_tile_override(int index) {
-  const int count = (int)(sizeof(tt::kTiles) / sizeof(tt::kTiles[0]));
-  TT_REQUIRE(index >= -1 && index < count, "gemm_tile_override: index %d out of [-1, %d)", index, count);
+  TT_REQUIRE(index >= -1 && index < tt::kNumTiles, "gemm_tile_override: index %d out of [-1, %d)",
+             index, tt::kNumTiles);
   tt::g_tile_override = index;
   return TT_OK;
 }
