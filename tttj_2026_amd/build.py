@@ -34,6 +34,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source flags.  The attention kernel reads its MFMA accumulators element-wise (softmax,
+# rescaling); keeping them in architectural VGPRs (instead of AGPRs) removes an AGPR <-> VGPR copy
+# per element per tile.
+SOURCE_FLAGS = {
+    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and pathlib.Path(cand).exists():
@@ -43,7 +51,8 @@ def hipcc() -> str:
 
 def _compile(src: pathlib.Path, extra) -> pathlib.Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o",
+           str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")
