@@ -63,9 +63,46 @@ int tt_device_count(void);
 int tt_weight_layout(int d_model, int ffn_dim, int num_layers, int64_t layer_offsets[12],
                      int64_t* layer_stride, int64_t* final_norm_offset, int64_t* total_elems);
 
-/* Bytes of workspace tt_transformer_fwd needs for this shape. */
-int tt_workspace_bytes(int batch, int seq, int d_model, int num_heads, int ffn_dim,
-                       int64_t* bytes);
+/* Execution plans of tt_transformer_fwd. */
+#define TT_PLAN_AUTO 0       /* megakernel for small token counts and d_model, else layer-wise */
+#define TT_PLAN_LAYERWISE 1  /* one launch per op: LN, GEMMs with fused epilogues, attention */
+#define TT_PLAN_MEGAKERNEL 2 /* one persistent cooperative launch for the whole stack */
+
+/* Bytes of workspace tt_transformer_fwd needs for this shape and plan.  The workspace of the
+ * megakernel plan holds its dependency counters and launch epoch: it must be zero-filled before
+ * its first use and then passed unchanged to every later call with the same shape (it is not
+ * re-entrant: calls that share it must be ordered on one stream).  Replaces the workspace
+ * allocation of fused_megakernel_forward / dag_megakernel_forward
+ * (kernels/fused_megakernel.py:1928-1937, kernels/dag_megakernel.py:2092-2097) and the persistent
+ * scheduler buffer of SequenceResidentTransformer (kernels/sequence_resident.py:148-150). */
+int tt_workspace_bytes(int batch, int seq, int d_model, int num_heads, int ffn_dim, int num_layers,
+                       int plan, int64_t* bytes);
+
+/* The plan TT_PLAN_AUTO resolves to for this shape (plan returned unchanged otherwise); < 0 on
+ * bad arguments.  Replaces the case dispatch of optimized_transformer.py:45-93. */
+int tt_resolve_plan(int batch, int seq, int d_model, int plan);
+
+/* Health word of a megakernel workspace (synchronises `stream`): *status = 0 when every
+ * dependency wait of every launch so far completed, 1 if some wait exceeded its bound (the
+ * outputs of that launch and later ones are then invalid and the workspace must be zero-filled
+ * again).  No counterpart in the reference, whose spin-waits are unbounded
+ * (kernels/dag_megakernel.py:1355-1367). */
+int tt_megakernel_status(const void* workspace, int batch, int seq, int d_model, int ffn_dim,
+                         int num_layers, int* status, void* stream);
+
+/* Number of DAG tasks of the megakernel plan for this shape (<0 on bad arguments). */
+int tt_megakernel_tasks(int batch, int seq, int d_model, int num_heads, int ffn_dim,
+                        int num_layers);
+
+/* tt_transformer_fwd with the megakernel plan, also writing a per-task trace: 4 uint64 words per
+ * task (task index | workgroup << 32, start, dependencies-satisfied, end; the times are the
+ * 100 MHz s_memrealtime clock) into the device buffer `trace` of `trace_words` words
+ * (>= 4 * tt_megakernel_tasks).  Replaces the CAPTURE trace slots of the reference's persistent
+ * kernels (kernels/fused_megakernel.py:20-26, 224-238). */
+int tt_megakernel_trace_fwd(const void* weights, const void* x, const uint8_t* mask, void* y,
+                            void* workspace, int64_t workspace_bytes, int batch, int seq,
+                            int d_model, int num_heads, int ffn_dim, int num_layers, int causal,
+                            uint64_t* trace, int64_t trace_words, void* stream);
 
 /* y[r] = LayerNorm(x[r]) * gamma + beta (eps, biased variance, fp32 statistics), fp16 out;
  * rows with valid[r] == 0 are written as +0.0 (valid may be NULL).  d % 8 == 0, d <= 8192.
@@ -110,10 +147,13 @@ int tt_attention_fwd(const void* q, const void* k, const void* vt, const uint8_t
  *   y = mask(final_norm(block_L(...block_1(x)))), block(x) = mask(x' + W2 gelu(W1 LN2(x') + b1)
  *   + b2) with x' = x + mask(Wo attn(LN1 x) + bo)
  * over the packed weights of tt_weight_layout.  x, y [B,S,D] fp16 (y must not alias x), mask
- * [B,S] bytes or NULL.  `plan` selects the execution strategy: 0 = automatic, 1 = layer-wise
- * kernels, 2 = persistent whole-model megakernel (only for shapes tt_megakernel_supported
- * accepts).  Replaces LayerwiseHybridTransformer.forward (kernels/layerwise_hybrid.py:255-361)
- * and SequenceResidentTransformer.run (kernels/sequence_resident.py:158-225). */
+ * [B,S] bytes or NULL.  `plan` is one of TT_PLAN_*: the layer-wise plan launches LN, the four
+ * GEMMs and attention per layer; the megakernel plan runs every layer in one cooperative launch
+ * whose workgroups hand work to each other through dependency counters.  Replaces
+ * LayerwiseHybridTransformer.forward (kernels/layerwise_hybrid.py:255-361),
+ * SequenceResidentTransformer.run (kernels/sequence_resident.py:158-225), fused_megakernel_forward
+ * (kernels/fused_megakernel.py:1860-2001) and dag_megakernel_forward
+ * (kernels/dag_megakernel.py:2060-2138). */
 int tt_transformer_fwd(const void* weights, const void* x, const uint8_t* mask, void* y,
                        void* workspace, int64_t workspace_bytes, int batch, int seq, int d_model,
                        int num_heads, int ffn_dim, int num_layers, int causal, int plan,

@@ -1,0 +1,100 @@
+"""Persistent megakernel plan (one cooperative launch, workgroup dependency DAG) against the fp32
+oracle and against the layer-wise plan.
+
+Same acceptance gate as the end-to-end tests (max-abs <= 2e-2, mean-abs <= 2e-3, padded rows
+bitwise +0.0).  Repeated launches on one workspace exercise the launch epoch (dependency counters
+are never reset), and the workspace health word must stay 0 (no dependency wait ran out).
+"""
+
+import copy
+
+import pytest
+import torch
+
+from oracle import transformer_oracle as O
+from tttj_2026_amd import PLAN_LAYERWISE, PLAN_MEGAKERNEL, make_optimized_transformer
+from tttj_2026_amd.configs import build_model, make_inputs
+from tttj_2026_amd.model import TransformerConfig
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # (B, S, D, H, F, L, causal, mask kind)
+    (1, 64, 256, 8, 1024, 4, True, None),          # C2 shape
+    (4, 128, 256, 4, 1024, 2, False, None),        # C1 shape
+    (3, 200, 256, 4, 512, 2, True, "prefix"),      # S not a multiple of the 128-row block
+    (2, 77, 256, 8, 256, 3, False, "nonprefix"),   # hd 32, ragged arbitrary mask
+    (2, 256, 512, 8, 2048, 2, True, "prefix"),     # two row blocks per sequence, hd 64
+    (5, 33, 128, 4, 128, 1, True, "empty"),        # the reference's own D = F shape family
+]
+
+
+def _mask(kind, b, s, seed):
+    if kind is None:
+        return None
+    g = torch.Generator().manual_seed(seed)
+    if kind == "prefix":
+        lens = torch.randint(max(1, s // 2), s + 1, (b,), generator=g)
+        return torch.arange(s)[None, :] < lens[:, None]
+    if kind == "empty":
+        lens = torch.randint(1, s + 1, (b,), generator=g)
+        lens[1] = 0                                  # one fully padded sequence
+        return torch.arange(s)[None, :] < lens[:, None]
+    m = torch.rand(b, s, generator=g) > 0.3
+    m[:, 0] = True
+    return m
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"B{c[0]}S{c[1]}D{c[2]}H{c[3]}F{c[4]}L{c[5]}"
+                                             f"{'c' if c[6] else 'n'}-{c[7]}" for c in CASES])
+def test_megakernel_parity_and_repeat(device, case):
+    b, s, d, h, f, l, causal, kind = case
+    cfg = TransformerConfig(b, s, d, h, f, l, causal)
+    model = build_model(cfg, seed=11)
+    with torch.no_grad():  # non-default LayerNorm affine parameters expose affine bugs
+        g = torch.Generator().manual_seed(12)
+        for name, p in model.named_parameters():
+            if "norm" in name:
+                p.add_(0.2 * torch.randn(p.shape, generator=g))
+    x16, _ = make_inputs(cfg, False, 13)
+    mask = _mask(kind, b, s, 14)
+    if mask is not None:
+        x16 = x16.masked_fill(~mask[..., None], 0)
+    gm = copy.deepcopy(model).half().to(device).eval()
+    mk = make_optimized_transformer(copy.deepcopy(gm), plan=PLAN_MEGAKERNEL)
+    lw = make_optimized_transformer(copy.deepcopy(gm), plan=PLAN_LAYERWISE)
+    xd = x16.to(device)
+    md = None if mask is None else mask.to(device)
+    print(f"[megakernel] case {case}", flush=True)
+    with torch.inference_mode():
+        outs = [mk(xd, md).clone() for _ in range(5)]
+        ref_lw = lw(xd, md)
+    torch.cuda.synchronize()
+    assert mk.megakernel_status(b, s) == 0
+    ref = O.forward(O.params_fp32(gm), x16.float(), mask, h, causal)
+    res = O.check_tolerance(outs[0], ref, mask)
+    assert res["passed"], res
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])           # deterministic across launches / epochs
+    res_lw = O.check_tolerance(ref_lw, ref, mask)
+    assert res_lw["passed"], res_lw
+    # both plans agree far inside the gate
+    assert (outs[0].float() - ref_lw.float()).abs().max().item() <= 2e-2
+
+
+def test_megakernel_workspace_survives_shape_changes(device):
+    """Alternate two (B, S) shapes on one module: each shape keeps its own workspace and epoch."""
+    cfg = TransformerConfig(2, 128, 256, 4, 1024, 2, True)
+    gm = build_model(cfg, seed=3).half().to(device).eval()
+    mk = make_optimized_transformer(copy.deepcopy(gm), plan=PLAN_MEGAKERNEL)
+    p32 = O.params_fp32(gm)
+    shapes = [(2, 128), (1, 50), (2, 128), (1, 50), (3, 64)]
+    for i, (b, s) in enumerate(shapes):
+        x16, mask = make_inputs(TransformerConfig(b, s, 256, 4, 1024, 2, True), True, 20 + i,
+                                min_valid=max(1, s // 3))
+        with torch.inference_mode():
+            y = mk(x16.to(device), mask.to(device))
+        torch.cuda.synchronize()
+        res = O.check_tolerance(y, O.forward(p32, x16.float(), mask, 4, True), mask)
+        assert res["passed"], (b, s, res)
+        assert mk.megakernel_status(b, s) == 0

@@ -63,6 +63,27 @@ def test_workspace_bytes_monotone_and_validated():
     assert big == pytest.approx((4 * 8192 * 1024 + 2 * 1024 * 4096 + 8192 * 4096) * 2, rel=1e-3)
     with pytest.raises(ValueError):
         _lib.workspace_bytes(1, 64, 256, 16, 1024)  # head_dim 16
+    # megakernel: residual, context, Q/K/V^T, FFN hidden (fp16) + counters growing with layers
+    m2 = _lib.workspace_bytes(1, 64, 256, 8, 1024, 2, _lib.PLAN_MEGAKERNEL)
+    m64 = _lib.workspace_bytes(1, 64, 256, 8, 1024, 64, _lib.PLAN_MEGAKERNEL)
+    assert (2 * 64 * 256 + 2 * 64 * 256 + 256 * 64 + 64 * 1024) * 2 < m2 < m64
+    with pytest.raises(ValueError):  # the LayerNorm'd operand of the megakernel lives in LDS
+        _lib.workspace_bytes(1, 64, 1024, 16, 4096, 2, _lib.PLAN_MEGAKERNEL)
+    with pytest.raises(ValueError):
+        _lib.workspace_bytes(1, 64, 256, 8, 1024, 2, 7)
+
+
+def test_plan_resolution():
+    # measured: the layer-wise plan is faster than the megakernel at C1 and C2 on MI355X
+    assert _lib.resolve_plan(1, 64, 256, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE      # C2
+    assert _lib.resolve_plan(4, 128, 256, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE     # C1
+    assert _lib.resolve_plan(1, 64, 256, _lib.PLAN_MEGAKERNEL) == _lib.PLAN_MEGAKERNEL
+    assert _lib.resolve_plan(8, 512, 512, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE     # C3
+    assert _lib.resolve_plan(2, 4096, 1024, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE   # C5
+    assert _lib.resolve_plan(1, 64, 1024, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE     # D > 512
+    assert _lib.resolve_plan(2, 4096, 512, _lib.PLAN_MEGAKERNEL) == _lib.PLAN_MEGAKERNEL
+    with pytest.raises(ValueError):
+        _lib.resolve_plan(1, 64, 256, 3)
 
 
 @pytest.mark.parametrize("kwargs,ok", [

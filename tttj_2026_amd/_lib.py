@@ -14,6 +14,7 @@ import threading
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libtttj_amd.so"
 
 TT_OK, TT_ERR_INVALID, TT_ERR_HIP = 0, 1, 2
+PLAN_AUTO, PLAN_LAYERWISE, PLAN_MEGAKERNEL = 0, 1, 2
 EPILOGUES = {"bias": 0, "gelu": 1, "resid_masked": 2, "masked_resid": 3, "qkv": 4}
 
 _P = ctypes.c_void_p
@@ -28,7 +29,12 @@ SIGNATURES = {
     "tt_device_count": (_I, []),
     "tt_weight_layout": (_I, [_I, _I, _I, ctypes.POINTER(_I64), ctypes.POINTER(_I64),
                               ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
-    "tt_workspace_bytes": (_I, [_I, _I, _I, _I, _I, ctypes.POINTER(_I64)]),
+    "tt_workspace_bytes": (_I, [_I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_I64)]),
+    "tt_resolve_plan": (_I, [_I, _I, _I, _I]),
+    "tt_megakernel_status": (_I, [_P, _I, _I, _I, _I, _I, ctypes.POINTER(_I), _P]),
+    "tt_megakernel_tasks": (_I, [_I, _I, _I, _I, _I, _I]),
+    "tt_megakernel_trace_fwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _I, _I, _P,
+                                     _I64, _P]),
     "tt_layernorm_fwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _P]),
     "tt_linear_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "tt_gemm_tile_override": (_I, [_I]),
@@ -87,8 +93,16 @@ def weight_layout(d_model: int, ffn_dim: int, num_layers: int):
     return list(offs), stride.value, final.value, total.value
 
 
-def workspace_bytes(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int) -> int:
+def workspace_bytes(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,
+                    num_layers: int = 1, plan: int = PLAN_LAYERWISE) -> int:
     out = _I64()
-    check(load().tt_workspace_bytes(batch, seq, d_model, heads, ffn_dim, ctypes.byref(out)),
-          "tt_workspace_bytes")
+    check(load().tt_workspace_bytes(batch, seq, d_model, heads, ffn_dim, num_layers, plan,
+                                    ctypes.byref(out)), "tt_workspace_bytes")
     return out.value
+
+
+def resolve_plan(batch: int, seq: int, d_model: int, plan: int) -> int:
+    rc = load().tt_resolve_plan(batch, seq, d_model, plan)
+    if rc < 0:
+        check(TT_ERR_INVALID, "tt_resolve_plan")
+    return rc

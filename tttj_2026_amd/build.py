@@ -39,6 +39,7 @@ HIPCC_FLAGS = [
 # per element per tile.
 SOURCE_FLAGS = {
     "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "megakernel.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

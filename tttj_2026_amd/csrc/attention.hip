@@ -1,283 +1,27 @@
-// Flash attention (online softmax) for head_dim 32 and 64 on gfx950, plus the per-sequence mask
-// summary it and the executor use.
-//
-// One 256-thread block owns (sequence b, head h, 128-query tile); each of its four waves owns 32
-// queries.  Key/value tiles of 64 keys are staged in LDS (double-buffered) by
-// global_load_lds_dwordx4 copies issued one tile ahead, so no registers hold in-flight tiles.
-// Per wave and tile:
-//   S^T = K Q^T   with v_mfma_f32_32x32x16_f16 (K from LDS as the A operand, Q^T held in
-//                 registers as the B operand), so lane l holds one query (l % 32) and 32 of the 64
-//                 keys: the row max and sum need one cross-half exchange (v_permlane32_swap);
-//   O^T += V^T P^T with V^T tiles from LDS (the QKV projection writes V transposed, [hd, S]).
-// To make the probabilities a lane already holds line up with 8 consecutive keys of V^T, K rows
-// are placed in LDS with bits 2 and 3 of the row index swapped: S^T row r then holds key pi(r),
-// and lane l of key block kb holds keys 32kb + 16(j/8) + 8(l/32) + (j%8), j = 0..15.
-// Softmax runs in the exp2 domain with scale*log2(e) folded into one FMA per score.  The running
-// max is refreshed lazily: the output is rescaled only when some row's max grows by more than
-// 2^8 over the reference max in use (exp2 of a score minus a stale reference is then at most 256,
-// exact in fp32 and in the fp16 probabilities).  Row sums add the fp16 probabilities that feed
-// the P V MFMA (v_dot2_f32_f16), so numerator and denominator use the same rounded values.
-// Masking: keys are dropped when key >= kv_end (last valid key + 1), when causal && key > query,
-// and, for masks that are not right-padded prefixes, when mask[b, key] == 0.  Query rows that are
-// padded are written as +0.0.  Causal query tiles are scheduled heaviest-first.
-#include "common.hpp"
+// Standalone flash-attention kernel (one block per (b, h, 128-query tile)) and the per-sequence
+// mask summary; the block itself is attention_block() in attention_block.hpp.
+#include "attention_block.hpp"
 #include "kernels.hpp"
 
 namespace tt {
 
-constexpr int kBQ = 128;
-constexpr int kBKV = 64;
-
-__host__ __device__ constexpr int round_up(int v, int m) { return (v + m - 1) / m * m; }
-
-__device__ __forceinline__ int pi23(int r) {  // swap bits 2 and 3
-  return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
-}
-
-// chunk swizzle for a K tile row of HD halfs (HD/8 chunks of 16 bytes)
-template <int HD>
-__device__ __forceinline__ int kswz(int row, int c) {
-  if constexpr (HD == 64) return c ^ (row & 7);
-  else return c ^ ((row >> 1) & 3);
-}
-
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ float xhalf_max(float v) {  // max over lanes l and l ^ 32
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
-__device__ __forceinline__ float xhalf_sum(float v) {  // sum over lanes l and l ^ 32
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-__device__ __forceinline__ void lds_copy16(const half* src, half* lds_dst) {
-  __builtin_amdgcn_global_load_lds((const void*)src,
-                                   (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
-}
-
 template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(256) void attention_kernel(
-    const half* __restrict__ Q, const half* __restrict__ K, const half* __restrict__ Vt,
-    const uint8_t* __restrict__ mask, const int32_t* __restrict__ info, half* __restrict__ ctx,
-    int B, int S, int H, float scale_log2) {
-  constexpr int KSTEPS = HD / 16;  // k-steps of the S^T MFMA
-  constexpr int DB = HD / 32;      // 32-row blocks of O^T
-  constexpr int KCH = HD / 8;      // 16-byte chunks per K row
-  constexpr int KRPC = 64 / KCH;   // K rows per 1 KiB copy
-  constexpr int KCOPIES = kBKV * HD * 2 / 1024 / 4;  // K copies per wave per tile
-  constexpr int VCOPIES = HD * kBKV * 2 / 1024 / 4;  // V^T copies per wave per tile
-  constexpr float kLazy = 8.0f;    // log2 growth of the row max that forces a rescale
-
-  __shared__ __align__(16) half sk[2][kBKV * HD];
-  __shared__ __align__(16) half sv[2][HD * kBKV];
-
-  const int BH = B * H;
-  const int nqt = (S + kBQ - 1) / kBQ;
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a, const int32_t* __restrict__ info) {
+  __shared__ __align__(16) half sk[2 * kBKV * HD];
+  __shared__ __align__(16) half sv[2 * HD * kBKV];
+  const int BH = a.B * a.H;
+  const int nqt = (a.S + kBQ - 1) / kBQ;
   const int bh = blockIdx.x % BH;
   int qt = blockIdx.x / BH;
-  if (CAUSAL) qt = nqt - 1 - qt;
-  const int b = bh / H, h = bh - b * H;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hf = lane >> 5, col = lane & 31;
-  const int ldv = round_up(S, kBKV);
-
-  int kv_end = S;
+  if (CAUSAL) qt = nqt - 1 - qt;  // heaviest causal tiles first
+  const int b = bh / a.H;
+  int kv_end = a.S;
   bool prefix = true;
   if (info != nullptr) {
     kv_end = info[b];
-    prefix = info[B + b] != 0;
+    prefix = info[a.B + b] != 0;
   }
-  const bool keymask = (mask != nullptr) && !prefix;
-
-  const int q0 = qt * kBQ;
-  const int qw = q0 + wave * 32;
-  const int q = qw + col;
-  const int block_end = CAUSAL ? min(kv_end, q0 + kBQ) : kv_end;
-  const int ntiles = (block_end + kBKV - 1) / kBKV;
-  const bool wave_active = qw < kv_end;  // queries >= kv_end are padded
-  const int wave_end = CAUSAL ? min(kv_end, qw + 32) : kv_end;
-
-  const size_t D = (size_t)H * HD;
-  const half* Qbh = Q + (size_t)bh * S * HD;
-  const half* Kbh = K + (size_t)bh * S * HD;
-  const half* Vbh = Vt + (size_t)bh * HD * ldv;
-
-  // Copy sources (per lane; the tile start is added per tile).  K copy c of this wave fills LDS
-  // rows p = (wave * KCOPIES + c) * KRPC + lane / KCH with key pi(p) at logical chunk
-  // (lane % KCH) ^ swizzle(p); V^T copy c fills row d = (wave * VCOPIES + c) * 8 + lane / 8 with
-  // keys 8 ((lane % 8) ^ (d % 8)) .. +7 of feature row d.
-  int krow[KCOPIES], koff[KCOPIES], voff[VCOPIES];
-#pragma unroll
-  for (int c = 0; c < KCOPIES; ++c) {
-    const int p = (wave * KCOPIES + c) * KRPC + lane / KCH;
-    krow[c] = (p & ~31) | pi23(p & 31);
-    koff[c] = kswz<HD>(p, lane % KCH) * 8;
-  }
-#pragma unroll
-  for (int c = 0; c < VCOPIES; ++c) {
-    const int d = (wave * VCOPIES + c) * 8 + (lane >> 3);
-    voff[c] = d * ldv + ((lane & 7) ^ (d & 7)) * 8;
-  }
-  auto issue_tile = [&](int t0, int st) {
-#pragma unroll
-    for (int c = 0; c < KCOPIES; ++c) {
-      const int key = min(t0 + krow[c], S - 1);  // rows past S load valid memory, never used
-      lds_copy16(Kbh + (size_t)key * HD + koff[c], &sk[st][(wave * KCOPIES + c) * 512]);
-    }
-#pragma unroll
-    for (int c = 0; c < VCOPIES; ++c)
-      lds_copy16(Vbh + voff[c] + t0, &sv[st][(wave * VCOPIES + c) * 512]);
-  };
-  // V^T columns of keys >= S (padding of the last, partial tile) are cleared in LDS so that
-  // 0-probability keys contribute 0 * 0, whatever the padding memory holds.
-  auto clear_vt_tail = [&](int t0, int st) {
-    const int first = S - t0;  // first invalid column of this tile, in (0, 64)
-    for (int e = tid; e < HD * kBKV; e += 256) {
-      const int d = e / kBKV, k = e % kBKV;
-      if (k >= first) sv[st][d * kBKV + swz(d, k / 8) * 8 + (k & 7)] = (half)0.f;
-    }
-  };
-
-  half8 qf[KSTEPS];
-#pragma unroll
-  for (int kk = 0; kk < KSTEPS; ++kk) {
-    if (q < S) qf[kk] = *(const half8*)(Qbh + (size_t)q * HD + 16 * kk + 8 * hf);
-    else
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qf[kk][e] = (half)0.f;
-  }
-
-  floatx16 o[DB];
-#pragma unroll
-  for (int i = 0; i < DB; ++i)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) o[i][e] = 0.f;
-  float m_ref = -INFINITY;  // reference max (log2 domain) the running sums are scaled to
-  float l_run = 0.f;        // this lane's half of the row sum
-
-  if (ntiles > 0) {
-    issue_tile(0, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (kBKV > S) {
-      clear_vt_tail(0, 0);
-      __syncthreads();
-    }
-  }
-  for (int t = 0; t < ntiles; ++t) {
-    const int st = t & 1;
-    const int t0 = t * kBKV;
-    if (t + 1 < ntiles) issue_tile(t0 + kBKV, st ^ 1);
-    if (wave_active && t0 < wave_end) {
-      floatx16 s[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
-        const int row = kb * 32 + col;
-#pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-          const half8 a = *(const half8*)(&sk[st][row * HD + kswz<HD>(row, 2 * kk + hf) * 8]);
-          s[kb] = mfma32x32x16(a, qf[kk], s[kb]);
-        }
-      }
-      const bool need_mask = (t0 + kBKV > kv_end) || (CAUSAL && t0 + kBKV - 1 > qw) || keymask;
-      if (need_mask) {
-        // Lane-local 32-bit "allowed" word, bit 16 kb + j for score s[kb][j] (key offset
-        // kr = 16 g + 8 hf + (j % 8) with g = 2 kb + j / 8): a range part (kr < lim - t0) and,
-        // for non-prefix masks, the bytes 2 g + hf of the tile's 64-key mask ballot.
-        const int lim = CAUSAL ? min(kv_end, q + 1) : kv_end;  // keys < lim may be valid
-        const int rem = lim - t0;
-        uint32_t allowed = 0;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = min(max(rem - (16 * g + 8 * hf), 0), 8);
-          allowed |= ((1u << n) - 1u) << (8 * g);
-        }
-        if (keymask) {
-          const int key = t0 + lane;
-          const uint64_t kbits = __ballot(key < S && mask[(size_t)b * S + key] != 0);
-          allowed &= __builtin_amdgcn_perm((uint32_t)(kbits >> 32), (uint32_t)kbits,
-                                           hf ? 0x07050301u : 0x06040200u);
-        }
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int j = 0; j < 16; ++j)
-            if (!((allowed >> (16 * kb + j)) & 1u)) s[kb][j] = -INFINITY;
-      }
-      float mx = s[0][0];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[kb][j]);
-      const float mt = xhalf_max(mx) * scale_log2;  // tile row max, log2 domain
-      if (__builtin_amdgcn_ballot_w64(mt > m_ref + kLazy) != 0) {
-        // Rescale: the new reference is the true running max (lanes whose max did not grow
-        // get corr = 1).  A row with no valid key so far keeps m_ref = -inf and o = l = 0.
-        const float m_new = fmaxf(m_ref, mt);
-        const float corr = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
-        m_ref = m_new;
-        l_run *= corr;
-#pragma unroll
-        for (int i = 0; i < DB; ++i)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) o[i][e] *= corr;
-      }
-      const float mc = (m_ref == -INFINITY) ? 0.f : m_ref;
-      half8 p16[2][2];
-      const half2v ones = {(half)1.f, (half)1.f};
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 16; j += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kb][j], scale_log2, -mc));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kb][j + 1], scale_log2, -mc));
-          const half2v pp = {(half)p0, (half)p1};
-          l_run = __builtin_amdgcn_fdot2(pp, ones, l_run, false);
-          p16[kb][j >> 3][j & 7] = pp[0];
-          p16[kb][j >> 3][(j & 7) + 1] = pp[1];
-        }
-#pragma unroll
-      for (int i = 0; i < DB; ++i) {
-        const int row = i * 32 + col;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            const half8 a = *(const half8*)(&sv[st][row * kBKV + swz(row, 4 * kb + 2 * c + hf) * 8]);
-            o[i] = mfma32x32x16(a, p16[kb][c], o[i]);
-          }
-      }
-    }
-    if (t + 1 < ntiles) {
-      __builtin_amdgcn_s_waitcnt(0);  // the next tile's copies have landed ...
-      __syncthreads();                // ... and every wave is done with this one
-      if (t0 + 2 * kBKV > S) {        // next tile is the partial last one
-        clear_vt_tail(t0 + kBKV, st ^ 1);
-        __syncthreads();
-      }
-    }
-  }
-
-  if (q >= S) return;
-  const float l_tot = xhalf_sum(l_run);
-  const bool qvalid = wave_active && q < kv_end && (mask == nullptr || mask[(size_t)b * S + q] != 0);
-  const float inv = (qvalid && l_tot > 0.f) ? 1.0f / l_tot : 0.f;
-  half* dst = ctx + ((size_t)b * S + q) * D + (size_t)h * HD;
-#pragma unroll
-  for (int i = 0; i < DB; ++i)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d = 32 * i + 8 * g + 4 * hf;
-      half4 v;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = qvalid ? (half)(o[i][4 * g + e] * inv) : (half)0.f;
-      *(half4*)(dst + d) = v;
-    }
+  attention_block<HD, CAUSAL>(a, bh, qt, kv_end, prefix, sk, sv);
 }
 
 __global__ __launch_bounds__(256) void mask_info_kernel(const uint8_t* __restrict__ mask,
@@ -332,9 +76,9 @@ int launch_attention(const half* q, const half* k, const half* vt, const uint8_t
   TT_REQUIRE(blocks < (1L << 31), "attention: grid too large");
   const float scale_log2 = (1.0f / sqrtf((float)head_dim)) * 1.4426950408889634f;
   const dim3 grid((unsigned)blocks), block(256);
-#define TT_ATT(HD, C)                                                                         \
-  hipLaunchKernelGGL((attention_kernel<HD, C>), grid, block, 0, stream, q, k, vt, mask, info, \
-                     ctx, batch, seq, heads, scale_log2)
+  const AttnArgs args{q, k, vt, mask, ctx, batch, seq, heads, scale_log2};
+#define TT_ATT(HD, C) \
+  hipLaunchKernelGGL((attention_kernel<HD, C>), grid, block, 0, stream, args, info)
   if (head_dim == 64) {
     if (causal) TT_ATT(64, true); else TT_ATT(64, false);
   } else {

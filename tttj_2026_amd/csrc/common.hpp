@@ -56,11 +56,40 @@ __device__ __forceinline__ floatx4 mfma16x16x32(half8 a, half8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+// Global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane l writes LDS bytes
+// [16 l, 16 l + 16) after the wave-uniform destination `lds_dst`.
+__device__ __forceinline__ void lds_copy16(const half* src, half* lds_dst) {
+  __builtin_amdgcn_global_load_lds((const void*)src,
+                                   (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over aligned groups of G lanes (G in {8, 16, 32, 64}), returned in every lane of the group.
+// VALU-only: DPP within 16-lane rows (xor 1, xor 2, half-mirror, mirror), then the gfx950 row
+// swaps v_permlane16_swap / v_permlane32_swap across rows (no LDS round trips).
+template <int G>
+__device__ __forceinline__ float seg_sum(float v) {
+  static_assert(G == 8 || G == 16 || G == 32 || G == 64, "group size");
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror: lanes i <-> 7 - i within 8
+  if constexpr (G >= 16) v += dpp_mov<0x140>(v);  // row_mirror: i <-> 15 - i within 16
+  if constexpr (G >= 32) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (G >= 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
   return v;
 }
+
+__device__ __forceinline__ float wave_sum(float v) { return seg_sum<64>(v); }
 
 __device__ __forceinline__ float gelu_erf(float v) {
   // Exact-erf GELU, F.gelu(approximate="none"): v * Phi(v), Phi(v) = erfc(-v / sqrt 2) / 2.

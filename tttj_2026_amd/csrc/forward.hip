@@ -113,13 +113,75 @@ extern "C" int tt_weight_layout(int d_model, int ffn_dim, int num_layers,
   return TT_OK;
 }
 
+// Token count up to which the automatic plan runs the persistent megakernel.  Measured on MI355X
+// (C1: B4 S128 D256, C2: B1 S64 D256) the megakernel is still slower than the layer-wise plan,
+// whose back-to-back launches pipeline with almost no gap, so the automatic choice is layer-wise
+// everywhere until that changes; the megakernel is selected explicitly with TT_PLAN_MEGAKERNEL.
+static constexpr int64_t kMegaMaxTokens = 0;
+static constexpr int kMegaMaxDModel = 512;  // the megakernel keeps a LayerNorm'd 64 x D tile in LDS
+
+static int resolve_plan(int plan, int B, int S, int D) {
+  if (plan != TT_PLAN_AUTO) return plan;
+  return ((int64_t)B * S <= kMegaMaxTokens && D <= kMegaMaxDModel) ? TT_PLAN_MEGAKERNEL
+                                                                    : TT_PLAN_LAYERWISE;
+}
+
 extern "C" int tt_workspace_bytes(int batch, int seq, int d_model, int num_heads, int ffn_dim,
-                                  int64_t* bytes) {
-  int rc = check_model_shape(batch, seq, d_model, num_heads, ffn_dim, 1);
+                                  int num_layers, int plan, int64_t* bytes) {
+  int rc = check_model_shape(batch, seq, d_model, num_heads, ffn_dim, num_layers);
   if (rc != TT_OK) return rc;
   TT_REQUIRE(bytes != nullptr, "workspace_bytes: null output");
-  *bytes = (int64_t)carve(nullptr, batch, seq, d_model, ffn_dim).bytes;
+  TT_REQUIRE(plan >= TT_PLAN_AUTO && plan <= TT_PLAN_MEGAKERNEL, "workspace_bytes: bad plan %d", plan);
+  plan = resolve_plan(plan, batch, seq, d_model);
+  if (plan == TT_PLAN_MEGAKERNEL) {
+    if ((rc = megakernel_supported(batch, seq, d_model, num_heads, ffn_dim, num_layers)) != TT_OK)
+      return rc;
+    *bytes = (int64_t)megakernel_workspace_bytes(batch, seq, d_model, ffn_dim, num_layers);
+  } else {
+    *bytes = (int64_t)carve(nullptr, batch, seq, d_model, ffn_dim).bytes;
+  }
   return TT_OK;
+}
+
+extern "C" int tt_resolve_plan(int batch, int seq, int d_model, int plan) {
+  if (plan < TT_PLAN_AUTO || plan > TT_PLAN_MEGAKERNEL || batch <= 0 || seq <= 0 || d_model <= 0) {
+    fail(TT_ERR_INVALID, "resolve_plan: bad arguments (batch=%d seq=%d d_model=%d plan=%d)",
+         batch, seq, d_model, plan);
+    return -1;
+  }
+  return resolve_plan(plan, batch, seq, d_model);
+}
+
+extern "C" int tt_megakernel_trace_fwd(const void* weights, const void* x, const uint8_t* mask,
+                                       void* y, void* workspace, int64_t workspace_bytes,
+                                       int batch, int seq, int d_model, int num_heads, int ffn_dim,
+                                       int num_layers, int causal, uint64_t* trace,
+                                       int64_t trace_words, void* stream) {
+  int rc = check_model_shape(batch, seq, d_model, num_heads, ffn_dim, num_layers);
+  if (rc != TT_OK) return rc;
+  TT_REQUIRE(weights && x && y && workspace && trace, "megakernel_trace_fwd: null pointer");
+  TT_REQUIRE(x != y, "megakernel_trace_fwd: y must not alias x");
+  const int64_t need = 4LL * megakernel_tasks(batch, seq, d_model, num_heads, ffn_dim, num_layers);
+  TT_REQUIRE(trace_words >= need, "megakernel_trace_fwd: trace holds %lld words, need %lld",
+             (long long)trace_words, (long long)need);
+  const Layout lay = weight_layout(d_model, ffn_dim, num_layers);
+  return launch_megakernel((const half*)weights, lay.off, lay.stride, lay.final_off,
+                           (const half*)x, mask, (half*)y, (char*)workspace, workspace_bytes,
+                           batch, seq, d_model, num_heads, ffn_dim, num_layers, causal,
+                           trace, (hipStream_t)stream);
+}
+
+extern "C" int tt_megakernel_tasks(int batch, int seq, int d_model, int num_heads, int ffn_dim,
+                                   int num_layers) {
+  if (check_model_shape(batch, seq, d_model, num_heads, ffn_dim, num_layers) != TT_OK) return -1;
+  return megakernel_tasks(batch, seq, d_model, num_heads, ffn_dim, num_layers);
+}
+
+extern "C" int tt_megakernel_status(const void* workspace, int batch, int seq, int d_model,
+                                    int ffn_dim, int num_layers, int* status, void* stream) {
+  TT_REQUIRE(workspace != nullptr && status != nullptr, "megakernel_status: null pointer");
+  return megakernel_status((const char*)workspace, batch, seq, d_model, ffn_dim, num_layers, status,
+                           (hipStream_t)stream);
 }
 
 extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint8_t* mask, void* y,
@@ -130,9 +192,15 @@ extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint
   if (rc != TT_OK) return rc;
   TT_REQUIRE(weights && x && y && workspace, "transformer: null pointer");
   TT_REQUIRE(x != y, "transformer: y must not alias x");
-  TT_REQUIRE(plan == 0 || plan == 1, "transformer: plan %d not available", plan);
+  TT_REQUIRE(plan >= TT_PLAN_AUTO && plan <= TT_PLAN_MEGAKERNEL, "transformer: bad plan %d", plan);
   const int B = batch, S = seq, D = d_model, H = num_heads, F = ffn_dim, L = num_layers;
   const int T = B * S, hd = D / H;
+  if (resolve_plan(plan, B, S, D) == TT_PLAN_MEGAKERNEL) {
+    const Layout lay = weight_layout(D, F, L);
+    return launch_megakernel((const half*)weights, lay.off, lay.stride, lay.final_off,
+                             (const half*)x, mask, (half*)y, (char*)workspace, workspace_bytes, B,
+                             S, D, H, F, L, causal, nullptr, (hipStream_t)stream_);
+  }
   Workspace ws = carve((char*)workspace, B, S, D, F);
   TT_REQUIRE((int64_t)ws.bytes <= workspace_bytes, "transformer: workspace %lld < %zu bytes",
              (long long)workspace_bytes, ws.bytes);

@@ -63,10 +63,6 @@ __device__ __forceinline__ half8 swap_halves(half8 t) {
 // [16 l, 16 l + 16) of an 8-row group, i.e. row l / 8, physical chunk l % 8.  The chunk swizzle is
 // applied on the global side: lane l fetches logical chunk (l % 8) ^ (l / 8) of its row, so the
 // physical chunk of logical chunk c in row r is c ^ (r % 8), as swz() expects.
-__device__ __forceinline__ void lds_copy16(const half* src, half* lds_dst) {
-  __builtin_amdgcn_global_load_lds((const void*)src,
-                                   (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
-}
 
 template <int BM, int BN, int MODE>
 __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,

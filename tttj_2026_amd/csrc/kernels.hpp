@@ -27,4 +27,16 @@ int launch_attention(const half* q, const half* k, const half* vt, const uint8_t
                      const int32_t* info, half* ctx, int batch, int seq, int heads, int head_dim,
                      int causal, hipStream_t stream);
 
+// Persistent whole-model megakernel (megakernel.hip).  The workspace must be zero-filled before
+// its first use and then reused unchanged between launches of the same shape.
+size_t megakernel_workspace_bytes(int B, int S, int D, int F, int L);
+int megakernel_supported(int B, int S, int D, int H, int F, int L);
+int launch_megakernel(const half* weights, const int64_t off[12], int64_t stride, int64_t final_off,
+                      const half* x, const uint8_t* mask, half* y, char* workspace,
+                      int64_t workspace_bytes, int B, int S, int D, int H, int F, int L, int causal,
+                      uint64_t* trace, hipStream_t stream);
+int megakernel_tasks(int B, int S, int D, int H, int F, int L);
+int megakernel_status(const char* workspace, int B, int S, int D, int F, int L, int* status,
+                      hipStream_t stream);
+
 }  // namespace tt

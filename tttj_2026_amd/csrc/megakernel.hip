@@ -1,0 +1,682 @@
+// Persistent whole-model megakernel: one cooperative launch runs every layer and the final norm,
+// with a workgroup-level dependency DAG in place of the per-op launches of the layer-wise plan.
+//
+// Tasks (row block rb = 64 consecutive tokens of one sequence; query block qb = 128 tokens):
+//   QKV(l, rb, nt)   LN1_l of the rows of rb (from x for l = 0, else the residual stream xa) is
+//                    computed straight into LDS, then 64 columns of [Q | K | V^T]
+//   ATT(l, b, h, qb) attention of query block qb of sequence b, head h -> ctx
+//   OUT(l, rb, nt)   xa[rb, nt] = resid + mask(ctx Wo^T + bo)
+//   FF1(l, rb, nt)   LN2_l of the rows of rb into LDS, then h[rb, nt] = GELU(LN2 W1^T + b1)
+//   FF2(l, rb, nt)   xa[rb, nt] = mask(xa + h W2^T + b2)
+//   FIN(rb)          y[rb] = mask(final_norm(xa[rb]))
+// A task computing LayerNorm reads complete rows written by other tasks, so it waits for all of
+// them; recomputing the norm in each of its consumers (instead of one task writing it out) keeps
+// it off the critical path and saves a global round trip.
+// Tasks are numbered in a topological order and handed out statically (task t to workgroup
+// t mod G).  Every task waits only on tasks numbered before it, and all G workgroups are
+// co-resident (cooperative launch), so the smallest unfinished task can always run: the DAG
+// cannot deadlock.  Dependencies are per (layer, kind, row block) counters in the workspace that
+// only ever grow; a launch waits for `epoch * count`, where the epoch (launch number) is kept in
+// the workspace and advanced by the last workgroup to finish, so no counter is ever reset (the
+// workspace must be zero-filled once, before its first use).  Hand-offs are agent-scope
+// release/acquire (the XCDs have separate L2s).  Every spin-wait is bounded: on expiry the kernel
+// records an error in the workspace and all later waits fall through, so every wave exits.
+//
+// Write-after-read: Q/K/V^T are single buffers, so QKV(l, rb) also waits for every attention
+// task of layer l-1 whose keys include rb.  Every other buffer's next writer already depends
+// (transitively) on its readers.
+//
+// The tasks are latency-bound (a 64 x 64 tile has 4 MFMAs per wave per K step), so the GEMM
+// tiles keep up to 8 K steps of copies in flight (global -> LDS, waited per step with vmcnt),
+// weights are prefetched before a task waits for its inputs, each task issues all of its memory
+// traffic as early as its dependencies allow, and LayerNorm row sums use DPP / lane-swap
+// reductions (no LDS round trips).
+#include "attention_block.hpp"
+#include "kernels.hpp"
+
+#include <algorithm>
+#include <cstring>
+#include <mutex>
+
+namespace tt {
+
+namespace {
+
+constexpr int kMB = 64;            // rows per row block
+constexpr int kQB = 128;           // queries per attention block (= attention_block's tile)
+constexpr int kNB = 64;            // columns per GEMM tile
+constexpr int kMaxD = 512;         // LN'd A operand resident in LDS: 64 x D halfs
+constexpr int kMKThreads = 256;
+constexpr uint32_t kSpinLimit = 1u << 22;
+
+// LDS map (halfs), 144 KiB + a small int area at the end.  Tasks whose A operand is a
+// LayerNorm computed in LDS (QKV, FF1) use [0, kResA) for it and a ring of kRingW weight-only K
+// steps after it; tasks that stream A (OUT, FF2) use the whole map as a ring of kRingAW steps of
+// A and W.  The attention tiles reuse the start of the map.
+constexpr int kResA = kMB * kMaxD;
+constexpr int kStepW = kNB * 64;            // one K step of W: 64 rows x 64 halfs
+constexpr int kStepAW = (kMB + kNB) * 64;   // one K step of A then W
+constexpr int kLdsHalfs = kResA + 10 * kStepW;
+constexpr int kRingW = 8;                   // K steps in flight (weights only)
+constexpr int kRingAW = kLdsHalfs / kStepAW;  // = 9
+static_assert(kResA + kRingW * kStepW <= kLdsHalfs && kRingAW * kStepAW <= kLdsHalfs, "LDS map");
+
+enum Counter : int { cQKV = 0, cATT, cOUT, cFF1, cFF2, kNumCounters };
+
+struct MegaParams {
+  const half* w;
+  int64_t off[12];
+  int64_t stride, final_off;
+  const half* x;
+  half* y;
+  const uint8_t* mask;
+  half *xa, *ctx, *q, *k, *vt, *hbuf;
+  uint32_t* cnt;    // [L * kNumCounters * nrb]
+  uint32_t* ctrl;   // [0] epoch, [1] finished workgroups, [2] error flag
+  uint64_t* trace;  // optional: 4 words per task (task | wg << 32, start, ready, end) or nullptr
+  int B, S, D, H, F, L, causal;
+  int nsb, nqb, nrb, tq, td, tf;  // row / query blocks per sequence, row blocks, N tiles
+  int per_layer, ntask;
+  float scale_log2;
+};
+
+__device__ __forceinline__ uint32_t ld_relaxed(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Trace stamps (100 MHz constant clock) of the task being run, written by thread 0 when a trace
+// buffer is given: start, dependencies satisfied ("ready"), end.
+__device__ __forceinline__ void trace_stamp(const MegaParams& p, int task, int slot) {
+  if (p.trace != nullptr && threadIdx.x == 0) {
+    uint64_t* rec = p.trace + 4 * (size_t)task;
+    if (slot == 1) rec[0] = (uint64_t)task | ((uint64_t)blockIdx.x << 32);
+    rec[slot] = __builtin_amdgcn_s_memrealtime();
+  }
+}
+
+__device__ __forceinline__ uint32_t* counter(const MegaParams& p, int layer, int kind, int rb) {
+  return p.cnt + ((size_t)layer * kNumCounters + kind) * p.nrb + rb;
+}
+
+// Block-wide: wait until *c has reached `target` (mod 2^32), bounded.
+__device__ void mk_wait(const MegaParams& p, const uint32_t* c, uint32_t target) {
+  if (threadIdx.x == 0) {
+    uint32_t spins = 0;
+    while ((int32_t)(ld_relaxed(c) - target) < 0) {
+      if (ld_relaxed(p.ctrl + 2) != 0) break;  // an earlier wait expired: fall through
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store(p.ctrl + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+// Block-wide: publish this block's writes and count one arrival on *c.
+__device__ void mk_signal(uint32_t* c) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// s_waitcnt on the vector-memory counter only: at most N loads of this wave still in flight.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+// Wait until at most `newer` (even, <= 28) of this wave's loads are still in flight.
+__device__ __forceinline__ void wait_newer(int newer) {
+  switch (newer >> 1) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<2>(); break;
+    case 2: wait_vmcnt<4>(); break;
+    case 3: wait_vmcnt<6>(); break;
+    case 4: wait_vmcnt<8>(); break;
+    case 5: wait_vmcnt<10>(); break;
+    case 6: wait_vmcnt<12>(); break;
+    case 7: wait_vmcnt<14>(); break;
+    case 8: wait_vmcnt<16>(); break;
+    case 9: wait_vmcnt<18>(); break;
+    case 10: wait_vmcnt<20>(); break;
+    case 11: wait_vmcnt<22>(); break;
+    case 12: wait_vmcnt<24>(); break;
+    case 13: wait_vmcnt<26>(); break;
+    default: wait_vmcnt<28>(); break;
+  }
+}
+static_assert(2 * (kRingW - 1) <= 28 && 4 * (kRingAW - 2) <= 28, "wait_newer range");
+
+// LayerNorm of the rows of one row block, G lanes per row (G >= D / 8 chunks of 8 halfs, so
+// 64 / G rows per wave instruction), every row's loads of a wave issued before any reduction.
+// OUT_LDS: write the normalised rows [0, 64) into the resident A area of LDS as
+// [D/64][64 rows][64 halfs] with 16-byte chunks swizzled by row (rows past nrows are zero);
+// otherwise write rows [0, nrows) to dst (global, row stride D), as +0.0 where the mask is 0.
+template <int G, bool OUT_LDS>
+__device__ void mk_layernorm_block(const half* src, const half* gamma, const half* beta,
+                                   const uint8_t* valid, int row0, int nrows, int D, half* dst) {
+  constexpr int RPP = 64 / G;                 // rows per wave pass
+  constexpr int PASSES = kMB / (4 * RPP);     // passes per wave (4 waves cover the 64 rows)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane % G;                     // this lane's 16-byte chunk of its row
+  const int nch = D >> 3;
+  const bool act = c < nch;
+  half8 g = {}, bb = {};
+  if (act) {
+    g = *(const half8*)(gamma + 8 * c);
+    bb = *(const half8*)(beta + 8 * c);
+  }
+  half8 v[PASSES];
+#pragma unroll
+  for (int i = 0; i < PASSES; ++i) {
+    const int r = (i * 4 + wave) * RPP + lane / G;
+    v[i] = half8{};
+    if (act && r < nrows) v[i] = *(const half8*)(src + (size_t)(row0 + r) * D + 8 * c);
+  }
+#pragma unroll
+  for (int i = 0; i < PASSES; ++i) {
+    const int r = (i * 4 + wave) * RPP + lane / G;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += (float)v[i][e];
+    const float mean = seg_sum<G>(s) / (float)D;
+    float qs = 0.f;
+    if (act) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float t = (float)v[i][e] - mean;
+        qs += t * t;
+      }
+    }
+    const float rstd = rsqrtf(seg_sum<G>(qs) / (float)D + 1e-5f);
+    if (!act) continue;
+    bool keep = r < nrows;
+    if constexpr (!OUT_LDS) keep = keep && (valid == nullptr || valid[row0 + r] != 0);
+    half8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      o[e] = keep ? (half)(((float)v[i][e] - mean) * rstd * (float)g[e] + (float)bb[e]) : (half)0.f;
+    if constexpr (OUT_LDS) {
+      *(half8*)(dst + ((c >> 3) * kMB + r) * 64 + (((c & 7) ^ (r & 7)) << 3)) = o;
+    } else if (r < nrows) {
+      *(half8*)(dst + (size_t)(row0 + r) * D + 8 * c) = o;
+    }
+  }
+}
+
+template <bool OUT_LDS>
+__device__ void mk_layernorm(const half* src, const half* gamma, const half* beta,
+                             const uint8_t* valid, int row0, int nrows, int D, half* dst) {
+  const int nch = D >> 3;
+  if (nch <= 8) mk_layernorm_block<8, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst);
+  else if (nch <= 16) mk_layernorm_block<16, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst);
+  else if (nch <= 32) mk_layernorm_block<32, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst);
+  else mk_layernorm_block<64, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst);
+}
+
+// ---- 64 x 64 GEMM tile, K streamed through an LDS ring of K steps ----
+// A K step holds [64 rows][64 halfs] per operand with 16-byte chunks swizzled by row.  Copy i of
+// a wave moves 8 rows (1 KiB): rows 8 (wave + 4 i) + lane / 8, logical chunk (lane % 8) ^ (row % 8).
+__device__ __forceinline__ void mk_copy_w(const half* W, int K, int n0, int k0, half* dst) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = (wave + 4 * i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ (lane >> 3);
+    lds_copy16(W + (size_t)(n0 + r) * K + k0 + 8 * c, dst + (wave + 4 * i) * 8 * 64);
+  }
+}
+
+__device__ __forceinline__ void mk_copy_a(const half* A, int K, int row0, int nrows, int k0,
+                                          half* dst) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = min((wave + 4 * i) * 8 + (lane >> 3), nrows - 1);  // clamped rows: never stored
+    const int c = (lane & 7) ^ (lane >> 3);
+    lds_copy16(A + (size_t)(row0 + r) * K + k0 + 8 * c, dst + (wave + 4 * i) * 8 * 64);
+  }
+}
+
+// Where K step s of a tile lives: RESA tiles keep W only, after the resident A area; streaming
+// tiles keep A then W, from the start of the map.
+template <bool RESA>
+struct Ring {
+  static constexpr int NS = RESA ? kRingW : kRingAW;
+  __device__ static half* w(half* lds, int s) {
+    return RESA ? lds + kResA + (s % NS) * kStepW : lds + (s % NS) * kStepAW + kMB * 64;
+  }
+  __device__ static half* a(half* lds, int s) { return lds + (s % NS) * kStepAW; }
+};
+
+// Issue the weight copies of the first min(NS - 1, nk) K steps (before the task waits for its
+// inputs: weights never change).
+template <bool RESA>
+__device__ __forceinline__ void mk_prefetch_w(const half* W, int K, int n0, half* lds) {
+  const int nk = K / 64;
+  for (int s = 0; s < Ring<RESA>::NS - 1 && s < nk; ++s) mk_copy_w(W, K, n0, s * 64, Ring<RESA>::w(lds, s));
+}
+
+// Y[row0 + m, n0 + n] for the 64 x 64 tile.  A comes from `A` (streamed, RESA == false) or from
+// the resident LayerNorm'd area (RESA == true).  The W copies of the first NS - 1 K steps must
+// have been issued by mk_prefetch_w<RESA>.  Four waves in 2 x 2, each a 32 x 32 MFMA block (W as
+// the A operand, so the accumulator is C^T).
+template <int MODE, bool RESA>
+__device__ void mk_gemm_tile(const half* A, const half* W, int K, int row0, int nrows, int n0,
+                             const EpiArgs& ep, half* lds) {
+  using R = Ring<RESA>;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int frow = lane & 31, fhi = lane >> 5, fx = lane & 7;
+  const int nk = K / 64;
+  constexpr bool RESID = MODE == TT_EPI_RESID_MASKED || MODE == TT_EPI_MASKED_RESID;
+  // Epilogue inputs first (their latency overlaps the main loop): residual and mask of this
+  // lane's row, 4 x 4 features.
+  const int ml = wm * 32 + frow;
+  const int mrow = row0 + min(ml, nrows - 1);
+  half4 res[4];
+  bool ok = true;
+  if constexpr (RESID) {
+    ok = ep.valid == nullptr || ep.valid[mrow] != 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      res[g] = *(const half4*)(ep.resid + (size_t)mrow * ep.ldy + n0 + wn * 32 + 8 * g + 4 * fhi);
+  }
+  const int pro = min(nk, R::NS - 1);  // K steps whose W copies mk_prefetch_w issued
+  if constexpr (!RESA) {
+    for (int s = 0; s < pro; ++s) mk_copy_a(A, K, row0, nrows, s * 64, R::a(lds, s));
+  }
+  floatx16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  // Issue order of this wave's loads: W copies of the prologue steps (mk_prefetch_w), then the
+  // residual loads, then the A copies of the prologue steps, then W and A of each later step
+  // together.  Step kt is complete once at most the loads issued after its last copy are in
+  // flight: `newer` counts those.
+  for (int kt = 0; kt < nk; ++kt) {
+    const int issued = min(nk, kt + R::NS - 1);  // steps whose copies are out
+    int newer;
+    if (RESA) newer = 2 * (issued - 1 - kt);
+    else if (kt < pro) newer = 2 * (pro - 1 - kt) + 4 * (issued - pro);
+    else newer = 4 * (issued - 1 - kt);
+    wait_newer(newer);
+    __syncthreads();  // step kt visible to all waves; step kt - 1's buffer is free
+    const int nxt = kt + R::NS - 1;
+    if (nxt < nk) {
+      mk_copy_w(W, K, n0, nxt * 64, R::w(lds, nxt));
+      if constexpr (!RESA) mk_copy_a(A, K, row0, nrows, nxt * 64, R::a(lds, nxt));
+    }
+    const half* wb = R::w(lds, kt);
+    const half* abase = RESA ? lds + kt * kMB * 64 : R::a(lds, kt);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int pc = (2 * kk + fhi) ^ fx;
+      const half8 b = *(const half8*)(abase + (wm * 32 + frow) * 64 + pc * 8);
+      const half8 a = *(const half8*)(wb + (wn * 32 + frow) * 64 + pc * 8);
+      acc = mfma32x32x16(a, b, acc);
+    }
+  }
+  __syncthreads();  // the ring and the resident area are free for the next task
+  // Epilogue straight from registers: acc[4g+e] = C[m][n], m = row0 + 32 wm + lane % 32,
+  // n = n0 + 32 wn + 8 g + 4 (lane / 32) + e.
+  if (ml >= nrows) return;
+  const int m = row0 + ml;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int n = n0 + wn * 32 + 8 * g + 4 * fhi;
+    const half4 bv = *(const half4*)(ep.bias + n);
+    half4 h;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float v = acc[4 * g + e] + (float)bv[e];
+      if constexpr (MODE == TT_EPI_BIAS_GELU) {
+        h[e] = (half)gelu_erf(v);
+      } else if constexpr (RESID) {
+        const half br = (half)v;  // branch rounded to fp16 first (eager boundary)
+        const half sum = (half)((float)res[g][e] + (float)br);
+        if constexpr (MODE == TT_EPI_RESID_MASKED) h[e] = ok ? sum : res[g][e];
+        else h[e] = ok ? sum : (half)0.f;
+      } else {
+        h[e] = (half)v;
+      }
+    }
+    if constexpr (MODE == TT_EPI_QKV) {
+      const int D = ep.d_model, hd = ep.head_dim, S = ep.seq;
+      const int which = n / D, nn = n - which * D;
+      const int hh = nn / hd, d = nn - hh * hd;
+      const int bb = m / S, sq = m - bb * S;
+      const size_t bh = (size_t)bb * ep.heads + hh;
+      const size_t plane = (size_t)ep.batch * S * D;
+      if (which < 2) {
+        *(half4*)(ep.y + which * plane + (bh * S + sq) * hd + d) = h;
+      } else {
+        const size_t ldv = (size_t)(S + 63) / 64 * 64;
+        half* vt = ep.y + 2 * plane + (bh * hd + d) * ldv + sq;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vt[(size_t)e * ldv] = h[e];
+      }
+    } else {
+      *(half4*)(ep.y + (size_t)m * ep.ldy + n) = h;
+    }
+  }
+}
+
+// kv_end (1 + last valid key) and prefix flag of sequence b, computed by the block.
+__device__ void mk_mask_summary(const MegaParams& p, int b, int* sred, int& kv_end, bool& prefix) {
+  if (p.mask == nullptr) {
+    kv_end = p.S;
+    prefix = true;
+    return;
+  }
+  int last = -1, count = 0;
+  for (int s = threadIdx.x; s < p.S; s += kMKThreads)
+    if (p.mask[(size_t)b * p.S + s]) {
+      last = s;
+      ++count;
+    }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    last = max(last, __shfl_xor(last, off, 64));
+    count += __shfl_xor(count, off, 64);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sred[wave] = last;
+    sred[4 + wave] = count;
+  }
+  __syncthreads();
+  last = max(max(sred[0], sred[1]), max(sred[2], sred[3]));
+  count = sred[4] + sred[5] + sred[6] + sred[7];
+  __syncthreads();
+  kv_end = last + 1;
+  prefix = count == last + 1;
+}
+
+template <int HD, bool CAUSAL>
+__global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
+  extern __shared__ __align__(16) half lds[];
+  half* resa = lds;
+  half* sk = lds;                     // attention tiles reuse the start of the map
+  half* sv = lds + 2 * kBKV * HD;
+  int* sred = (int*)(lds + kLdsHalfs);
+
+  const uint32_t epoch = ld_relaxed(p.ctrl) + 1u;  // this launch's number (workspace starts at 0)
+  const AttnArgs aa{p.q, p.k, p.vt, p.mask, p.ctx, p.B, p.S, p.H, p.scale_log2};
+
+  for (int t = blockIdx.x; t < p.ntask; t += gridDim.x) {
+    trace_stamp(p, t, 1);
+    if (t >= p.L * p.per_layer) {  // FIN(rb)
+      const int rb = t - p.L * p.per_layer, b = rb / p.nsb, sb = rb - b * p.nsb;
+      const int row0 = b * p.S + sb * kMB, nrows = min(kMB, p.S - sb * kMB);
+      mk_wait(p, counter(p, p.L - 1, cFF2, rb), epoch * (uint32_t)p.td);
+      trace_stamp(p, t, 2);
+      {
+        const int64_t dpad = (p.D + 63) / 64 * 64;
+        mk_layernorm<false>(p.xa, p.w + p.final_off, p.w + p.final_off + dpad, p.mask, row0, nrows,
+                            p.D, p.y);
+      }
+      __syncthreads();
+      trace_stamp(p, t, 3);
+      continue;
+    }
+    // ---- decode task t
+    const int l = t / p.per_layer;
+    int i0 = t - l * p.per_layer;
+    int kind = 0;
+    {
+      const int seg[5] = {p.nrb * p.tq, p.B * p.H * p.nqb, p.nrb * p.td, p.nrb * p.tf, p.nrb * p.td};
+      while (kind < 4 && i0 >= seg[kind]) i0 -= seg[kind++];
+    }
+    const half* wl = p.w + (size_t)l * p.stride;
+
+    if (kind == 1) {  // ATT(l, b, h, qb): heaviest query blocks first when causal
+      const int bh = i0 / p.nqb;
+      int qb = i0 - bh * p.nqb;
+      if (CAUSAL) qb = p.nqb - 1 - qb;
+      const int b = bh / p.H;
+      int kv_end;
+      bool prefix;
+      mk_mask_summary(p, b, sred, kv_end, prefix);
+      const int q_hi = min(p.S, (qb + 1) * kQB);
+      const int key_hi = CAUSAL ? min(kv_end, q_hi) : kv_end;
+      const int need = (max(key_hi, q_hi) + kMB - 1) / kMB;  // row blocks of keys and queries
+      for (int j = 0; j < need; ++j)
+        mk_wait(p, counter(p, l, cQKV, b * p.nsb + j), epoch * (uint32_t)p.tq);
+      trace_stamp(p, t, 2);
+      attention_block<HD, CAUSAL>(aa, bh, qb, kv_end, prefix, sk, sv);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      __syncthreads();
+      if (threadIdx.x == 0)
+        for (int j = 2 * qb; j < min(2 * qb + 2, p.nsb); ++j)
+          __hip_atomic_fetch_add(counter(p, l, cATT, b * p.nsb + j), 1u, __ATOMIC_RELEASE,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      trace_stamp(p, t, 3);
+      continue;
+    }
+
+    // GEMM tasks: i0 = rb * tiles + nt
+    const int tiles = (kind == 0) ? p.tq : (kind == 3) ? p.tf : p.td;
+    const int rb = i0 / tiles, nt = i0 - rb * tiles;
+    const int b = rb / p.nsb, sb = rb - b * p.nsb;
+    const int row0 = b * p.S + sb * kMB, nrows = min(kMB, p.S - sb * kMB);
+    const int n0 = nt * kNB;
+    EpiArgs ep{};
+    if (kind == 0) {  // QKV
+      const half* W = wl + p.off[2];
+      mk_prefetch_w<true>(W, p.D, n0, lds);
+      if (l > 0) {
+        mk_wait(p, counter(p, l - 1, cFF2, rb), epoch * (uint32_t)p.td);
+        // write-after-read on Q/K/V^T: attention of layer l-1 reading rows rb is done
+        for (int j = CAUSAL ? (sb & ~1) : 0; j < p.nsb; j += 2)
+          mk_wait(p, counter(p, l - 1, cATT, b * p.nsb + j), epoch * (uint32_t)p.H);
+      }
+      trace_stamp(p, t, 2);
+      mk_layernorm<true>(l == 0 ? p.x : p.xa, wl + p.off[0], wl + p.off[1], nullptr, row0, nrows,
+                         p.D, resa);
+      ep.bias = wl + p.off[3];
+      ep.y = p.q;
+      ep.ldy = 3 * p.D;
+      ep.mode = TT_EPI_QKV;
+      ep.batch = p.B;
+      ep.seq = p.S;
+      ep.heads = p.H;
+      ep.head_dim = HD;
+      ep.d_model = p.D;
+      mk_gemm_tile<TT_EPI_QKV, true>(nullptr, W, p.D, row0, nrows, n0, ep, lds);
+      mk_signal(counter(p, l, cQKV, rb));
+    } else if (kind == 2) {  // OUT
+      const half* W = wl + p.off[4];
+      mk_prefetch_w<false>(W, p.D, n0, lds);
+      mk_wait(p, counter(p, l, cATT, rb), epoch * (uint32_t)p.H);
+      trace_stamp(p, t, 2);
+      ep.bias = wl + p.off[5];
+      ep.resid = (l == 0) ? p.x : p.xa;
+      ep.valid = p.mask;
+      ep.y = p.xa;
+      ep.ldy = p.D;
+      ep.mode = TT_EPI_RESID_MASKED;
+      mk_gemm_tile<TT_EPI_RESID_MASKED, false>(p.ctx, W, p.D, row0, nrows, n0, ep, lds);
+      mk_signal(counter(p, l, cOUT, rb));
+    } else if (kind == 3) {  // FF1
+      const half* W = wl + p.off[8];
+      mk_prefetch_w<true>(W, p.D, n0, lds);
+      mk_wait(p, counter(p, l, cOUT, rb), epoch * (uint32_t)p.td);
+      trace_stamp(p, t, 2);
+      mk_layernorm<true>(p.xa, wl + p.off[6], wl + p.off[7], nullptr, row0, nrows, p.D, resa);
+      ep.bias = wl + p.off[9];
+      ep.y = p.hbuf;
+      ep.ldy = p.F;
+      ep.mode = TT_EPI_BIAS_GELU;
+      mk_gemm_tile<TT_EPI_BIAS_GELU, true>(nullptr, W, p.D, row0, nrows, n0, ep, lds);
+      mk_signal(counter(p, l, cFF1, rb));
+    } else {  // FF2
+      const half* W = wl + p.off[10];
+      mk_prefetch_w<false>(W, p.F, n0, lds);
+      mk_wait(p, counter(p, l, cFF1, rb), epoch * (uint32_t)p.tf);
+      trace_stamp(p, t, 2);
+      ep.bias = wl + p.off[11];
+      ep.resid = p.xa;
+      ep.valid = p.mask;
+      ep.y = p.xa;
+      ep.ldy = p.D;
+      ep.mode = TT_EPI_MASKED_RESID;
+      mk_gemm_tile<TT_EPI_MASKED_RESID, false>(p.hbuf, W, p.F, row0, nrows, n0, ep, lds);
+      mk_signal(counter(p, l, cFF2, rb));
+    }
+    trace_stamp(p, t, 3);
+  }
+
+  // The last workgroup to finish advances the epoch for the next launch and clears the
+  // finish count (every workgroup read the epoch before it arrives here; the next launch is
+  // stream-ordered after this one).
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(p.ctrl + 1, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (old + 1u == gridDim.x) {
+      __hip_atomic_store(p.ctrl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.ctrl, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+}  // namespace
+
+// ---- host side ----
+
+struct MegaLayout {
+  size_t xa, ctx, qkv, hbuf, cnt, ctrl, bytes;
+};
+
+static size_t al256(size_t v) { return (v + 255) / 256 * 256; }
+
+static MegaLayout mega_layout(int64_t B, int64_t S, int64_t D, int64_t F, int64_t L) {
+  const int64_t T = B * S, Sp = (S + 63) / 64 * 64, nrb = B * ((S + kMB - 1) / kMB);
+  MegaLayout m{};
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += al256(bytes);
+    return at;
+  };
+  m.xa = take(T * D * 2);
+  m.ctx = take(T * D * 2);
+  m.qkv = take((2 * T * D + B * D * Sp) * 2);
+  m.hbuf = take(T * F * 2);
+  m.cnt = take((size_t)L * kNumCounters * nrb * 4);
+  m.ctrl = take(64);
+  m.bytes = o;
+  return m;
+}
+
+size_t megakernel_workspace_bytes(int B, int S, int D, int F, int L) {
+  return mega_layout(B, S, D, F, L).bytes;
+}
+
+int megakernel_supported(int B, int S, int D, int H, int F, int L) {
+  TT_REQUIRE(D / H == 32 || D / H == 64, "megakernel: head_dim %d not in {32, 64}", D / H);
+  TT_REQUIRE(D % 64 == 0 && F % 64 == 0, "megakernel: d_model and ffn_dim must be multiples of 64");
+  TT_REQUIRE(D <= kMaxD, "megakernel: d_model %d > %d (the LayerNorm'd operand lives in LDS)", D,
+             kMaxD);
+  TT_REQUIRE((int64_t)B * S <= (1 << 20), "megakernel: too many tokens for the persistent plan");
+  (void)L;
+  return TT_OK;
+}
+
+template <int HD, bool CAUSAL>
+static int launch_mega(MegaParams& p, hipStream_t stream) {
+  const size_t lds = kLdsHalfs * sizeof(half) + 64;
+  static_assert(2 * kBKV * HD * 2 <= kLdsHalfs, "attention tiles must fit the LDS map");
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  static int per_cu = 0;
+  std::call_once(once, [&] {
+    attr = hipFuncSetAttribute((const void*)megakernel<HD, CAUSAL>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr == hipSuccess)
+      attr = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, megakernel<HD, CAUSAL>,
+                                                          kMKThreads, lds);
+  });
+  if (attr != hipSuccess) return fail(TT_ERR_HIP, "megakernel setup: %s", hipGetErrorString(attr));
+  int dev = 0, cus = 0;
+  TT_HIP(hipGetDevice(&dev));
+  TT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  // As many workgroups as the widest stage has tasks, within what can be co-resident.
+  const int widest = std::max({p.nrb * p.tq, p.B * p.H * p.nqb, p.nrb * p.tf, p.nrb * p.td});
+  int grid = std::min(widest, cus * std::max(per_cu, 1));
+  grid = std::max(1, std::min(grid, cus));
+  void* args[] = {&p};
+  TT_HIP(hipLaunchCooperativeKernel((const void*)megakernel<HD, CAUSAL>, dim3(grid),
+                                    dim3(kMKThreads), args, lds, stream));
+  return TT_OK;
+}
+
+int megakernel_tasks(int B, int S, int D, int H, int F, int L) {
+  const int nsb = (S + kMB - 1) / kMB, nrb = B * nsb, nqb = (S + kQB - 1) / kQB;
+  const int per_layer = nrb * (3 * D / kNB) + B * H * nqb + nrb * (D / kNB) + nrb * (F / kNB) +
+                        nrb * (D / kNB);
+  return L * per_layer + nrb;
+}
+
+int launch_megakernel(const half* weights, const int64_t off[12], int64_t stride, int64_t final_off,
+                      const half* x, const uint8_t* mask, half* y, char* workspace,
+                      int64_t workspace_bytes, int B, int S, int D, int H, int F, int L, int causal,
+                      uint64_t* trace, hipStream_t stream) {
+  int rc = megakernel_supported(B, S, D, H, F, L);
+  if (rc != TT_OK) return rc;
+  const MegaLayout m = mega_layout(B, S, D, F, L);
+  TT_REQUIRE((int64_t)m.bytes <= workspace_bytes, "megakernel: workspace %lld < %zu bytes",
+             (long long)workspace_bytes, m.bytes);
+  MegaParams p{};
+  p.w = weights;
+  memcpy(p.off, off, sizeof(p.off));
+  p.stride = stride;
+  p.final_off = final_off;
+  p.x = x;
+  p.y = y;
+  p.mask = mask;
+  p.xa = (half*)(workspace + m.xa);
+  p.ctx = (half*)(workspace + m.ctx);
+  p.q = (half*)(workspace + m.qkv);
+  p.k = p.q + (size_t)B * S * D;
+  p.vt = p.q + 2 * (size_t)B * S * D;
+  p.hbuf = (half*)(workspace + m.hbuf);
+  p.cnt = (uint32_t*)(workspace + m.cnt);
+  p.ctrl = (uint32_t*)(workspace + m.ctrl);
+  p.trace = trace;
+  p.B = B;
+  p.S = S;
+  p.D = D;
+  p.H = H;
+  p.F = F;
+  p.L = L;
+  p.causal = causal;
+  p.nsb = (S + kMB - 1) / kMB;
+  p.nqb = (S + kQB - 1) / kQB;
+  p.nrb = B * p.nsb;
+  p.tq = 3 * D / kNB;
+  p.td = D / kNB;
+  p.tf = F / kNB;
+  p.per_layer = p.nrb * p.tq + B * H * p.nqb + p.nrb * p.td + p.nrb * p.tf + p.nrb * p.td;
+  p.ntask = L * p.per_layer + p.nrb;
+  p.scale_log2 = (1.0f / sqrtf((float)(D / H))) * 1.4426950408889634f;
+  const int hd = D / H;
+  if (hd == 64) return causal ? launch_mega<64, true>(p, stream) : launch_mega<64, false>(p, stream);
+  return causal ? launch_mega<32, true>(p, stream) : launch_mega<32, false>(p, stream);
+}
+
+int megakernel_status(const char* workspace, int B, int S, int D, int F, int L, int* status,
+                      hipStream_t stream) {
+  const MegaLayout m = mega_layout(B, S, D, F, L);
+  uint32_t ctrl[3] = {0, 0, 0};
+  TT_HIP(hipMemcpyAsync(ctrl, workspace + m.ctrl, sizeof(ctrl), hipMemcpyDeviceToHost, stream));
+  TT_HIP(hipStreamSynchronize(stream));
+  *status = (int)ctrl[2];
+  return TT_OK;
+}
+
+}  // namespace tt

@@ -9,13 +9,19 @@ any work, as the reference does for unsupported shapes.
 
 The module packs the parameter model's fp16 weights once (``prepare``) into the layout of
 ``tt_weight_layout`` and runs every forward as one call into the HIP library on the caller's
-current stream.  It returns a fresh output tensor per call; repeated calls on the same inputs are
-bit-identical.  A module instance owns one workspace per (batch, seq) and is not re-entrant across
-streams.
+current stream: either the layer-wise plan (LN, four GEMMs with fused epilogues and attention per
+layer) or, for small token counts, the persistent megakernel (one cooperative launch for the whole
+stack, workgroups handing work to each other through dependency counters); ``plan`` forces one.
+It returns a fresh output tensor per call; repeated calls on the same inputs are bit-identical.
+A module instance owns one workspace per (batch, seq, plan) -- for the megakernel it holds the
+dependency counters and launch epoch, so it is zero-filled once and then reused -- and is not
+re-entrant across streams (the reference's scheduler buffer has the same contract,
+kernels/sequence_resident.py:148-150).
 """
 
 from __future__ import annotations
 
+import ctypes
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -23,7 +29,7 @@ import torch.nn as nn
 
 from . import _lib
 
-PLAN_AUTO, PLAN_LAYERWISE, PLAN_MEGAKERNEL = 0, 1, 2
+PLAN_AUTO, PLAN_LAYERWISE, PLAN_MEGAKERNEL = _lib.PLAN_AUTO, _lib.PLAN_LAYERWISE, _lib.PLAN_MEGAKERNEL
 
 
 def check_supported(config) -> None:
@@ -101,11 +107,13 @@ class OptimizedTransformer(nn.Module):
 
     def __init__(self, parameter_model: nn.Module, plan: int = PLAN_AUTO) -> None:
         super().__init__()
+        if plan not in (PLAN_AUTO, PLAN_LAYERWISE, PLAN_MEGAKERNEL):
+            raise ValueError(f"unknown plan {plan}")
         self.parameter_model = parameter_model
         self.config = parameter_model.config
         self.plan = plan
         self.register_buffer("packed_weights", None, persistent=False)
-        self._workspaces: Dict[Tuple[int, int, int], torch.Tensor] = {}
+        self._workspaces: Dict[Tuple[int, int, int, int], torch.Tensor] = {}
 
     def prepare(self) -> None:
         check_supported(self.config)
@@ -113,15 +121,58 @@ class OptimizedTransformer(nn.Module):
         self.packed_weights = pack_model_weights(self.parameter_model)
         self._lib = lib
 
-    def _workspace(self, batch: int, seq: int, device: torch.device) -> torch.Tensor:
-        key = (batch, seq, device.index if device.index is not None else 0)
+    def _workspace(self, batch: int, seq: int, plan: int, device: torch.device) -> torch.Tensor:
+        key = (batch, seq, plan, device.index if device.index is not None else 0)
         ws = self._workspaces.get(key)
         if ws is None:
             cfg = self.config
-            nbytes = _lib.workspace_bytes(batch, seq, cfg.d_model, cfg.num_heads, cfg.ffn_dim)
-            ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            nbytes = _lib.workspace_bytes(batch, seq, cfg.d_model, cfg.num_heads, cfg.ffn_dim,
+                                          cfg.num_layers, plan)
+            # zero-filled: the megakernel's dependency counters and epoch must start at 0
+            ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
             self._workspaces[key] = ws
         return ws
+
+    def forward_traced(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None):
+        """Megakernel forward that also returns its per-task trace: an int64 [tasks, 4] CPU
+        tensor of (task | workgroup << 32, start, ready, end) on the GPU's 100 MHz clock, where
+        `ready` is when the task's dependencies were satisfied (tracing of the persistent plan,
+        after the reference's capture slots, kernels/fused_megakernel.py:20-26)."""
+        if self.packed_weights is None:
+            self.prepare()
+        cfg = self.config
+        x = x.contiguous()
+        batch, seq, _ = x.shape
+        mask = None if valid_token_mask is None else valid_token_mask.contiguous()
+        ntask = self._lib.tt_megakernel_tasks(batch, seq, cfg.d_model, cfg.num_heads, cfg.ffn_dim,
+                                              cfg.num_layers)
+        if ntask < 0:
+            raise ValueError(f"tt_megakernel_tasks: {_lib.last_error()}")
+        trace = torch.zeros(4 * ntask, dtype=torch.int64, device=x.device)
+        ws = self._workspace(batch, seq, PLAN_MEGAKERNEL, x.device)
+        y = torch.empty_like(x)
+        rc = self._lib.tt_megakernel_trace_fwd(
+            self.packed_weights.data_ptr(), x.data_ptr(), None if mask is None else mask.data_ptr(),
+            y.data_ptr(), ws.data_ptr(), ws.numel(), batch, seq, cfg.d_model, cfg.num_heads,
+            cfg.ffn_dim, cfg.num_layers, int(bool(cfg.causal)), trace.data_ptr(), trace.numel(),
+            torch.cuda.current_stream(x.device).cuda_stream)
+        _lib.check(rc, "tt_megakernel_trace_fwd")
+        return y, trace.view(ntask, 4).cpu()
+
+    def megakernel_status(self, batch: int, seq: int) -> int:
+        """0 if every dependency wait of the megakernel workspace for (batch, seq) completed so
+        far, 1 if one exceeded its bound (synchronises the current stream)."""
+        cfg = self.config
+        dev = self.packed_weights.device
+        ws = self._workspaces.get((batch, seq, PLAN_MEGAKERNEL, dev.index or 0))
+        if ws is None:
+            return 0
+        status = ctypes.c_int(0)
+        _lib.check(self._lib.tt_megakernel_status(
+            ws.data_ptr(), batch, seq, cfg.d_model, cfg.ffn_dim, cfg.num_layers,
+            ctypes.byref(status), torch.cuda.current_stream(dev).cuda_stream),
+            "tt_megakernel_status")
+        return status.value
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None):
         if self.packed_weights is None:
@@ -146,12 +197,13 @@ class OptimizedTransformer(nn.Module):
         y = torch.empty_like(x)
         if batch * seq == 0:
             return y
-        ws = self._workspace(batch, seq, x.device)
+        plan = _lib.resolve_plan(batch, seq, cfg.d_model, self.plan)
+        ws = self._workspace(batch, seq, plan, x.device)
         stream = torch.cuda.current_stream(x.device).cuda_stream
         rc = self._lib.tt_transformer_fwd(
             self.packed_weights.data_ptr(), x.data_ptr(), mask_ptr, y.data_ptr(), ws.data_ptr(),
             ws.numel(), batch, seq, cfg.d_model, cfg.num_heads, cfg.ffn_dim, cfg.num_layers,
-            int(bool(cfg.causal)), self.plan, stream)
+            int(bool(cfg.causal)), plan, stream)
         _lib.check(rc, "tt_transformer_fwd")
         return y
 
