@@ -66,7 +66,7 @@ int tt_weight_layout(int d_model, int ffn_dim, int num_layers, int64_t layer_off
 /* Execution plans of tt_transformer_fwd. */
 #define TT_PLAN_AUTO 0       /* megakernel for small token counts and d_model, else layer-wise */
 #define TT_PLAN_LAYERWISE 1  /* one launch per op: LN, GEMMs with fused epilogues, attention */
-#define TT_PLAN_MEGAKERNEL 2 /* one persistent cooperative launch for the whole stack */
+#define TT_PLAN_MEGAKERNEL 2 /* one persistent launch (<= one workgroup per CU) for the stack */
 
 /* Bytes of workspace tt_transformer_fwd needs for this shape and plan.  The workspace of the
  * megakernel plan holds its dependency counters and launch epoch: it must be zero-filled before
@@ -148,8 +148,10 @@ int tt_attention_fwd(const void* q, const void* k, const void* vt, const uint8_t
  *   + b2) with x' = x + mask(Wo attn(LN1 x) + bo)
  * over the packed weights of tt_weight_layout.  x, y [B,S,D] fp16 (y must not alias x), mask
  * [B,S] bytes or NULL.  `plan` is one of TT_PLAN_*: the layer-wise plan launches LN, the four
- * GEMMs and attention per layer; the megakernel plan runs every layer in one cooperative launch
- * whose workgroups hand work to each other through dependency counters.  Replaces
+ * GEMMs and attention per layer; the megakernel plan runs every layer in one launch of at most
+ * one workgroup per CU, whose workgroups hand work to each other through dependency counters
+ * (it relies on all of them being resident, i.e. on the device not being shared with other
+ * kernels while it runs; its waits are bounded, see tt_megakernel_status).  Replaces
  * LayerwiseHybridTransformer.forward (kernels/layerwise_hybrid.py:255-361),
  * SequenceResidentTransformer.run (kernels/sequence_resident.py:158-225), fused_megakernel_forward
  * (kernels/fused_megakernel.py:1860-2001) and dag_megakernel_forward

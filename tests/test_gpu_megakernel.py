@@ -1,4 +1,4 @@
-"""Persistent megakernel plan (one cooperative launch, workgroup dependency DAG) against the fp32
+"""Persistent megakernel plan (one persistent launch, workgroup dependency DAG) against the fp32
 oracle and against the layer-wise plan.
 
 Same acceptance gate as the end-to-end tests (max-abs <= 2e-2, mean-abs <= 2e-3, padded rows

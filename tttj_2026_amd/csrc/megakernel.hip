@@ -1,4 +1,4 @@
-// Persistent whole-model megakernel: one cooperative launch runs every layer and the final norm,
+// Persistent whole-model megakernel: one launch runs every layer and the final norm,
 // with a workgroup-level dependency DAG in place of the per-op launches of the layer-wise plan.
 //
 // Tasks (row block rb = 64 consecutive tokens of one sequence; query block qb = 128 tokens):
@@ -14,8 +14,11 @@
 // it off the critical path and saves a global round trip.
 // Tasks are numbered in a topological order and handed out statically (task t to workgroup
 // t mod G).  Every task waits only on tasks numbered before it, and all G workgroups are
-// co-resident (cooperative launch), so the smallest unfinished task can always run: the DAG
-// cannot deadlock.  Dependencies are per (layer, kind, row block) counters in the workspace that
+// resident at once, so the smallest unfinished task can always run: the DAG cannot deadlock.
+// Residency comes from the launch size: G <= the number of CUs and a workgroup's 144 KiB of LDS
+// fits one per CU, so on a device not shared with other kernels every workgroup is dispatched at
+// once.  (A cooperative launch would guarantee it formally but costs ~17 us more per launch on
+// MI355X -- measured -- which is more than the forward of the small shapes this plan is for.)  Dependencies are per (layer, kind, row block) counters in the workspace that
 // only ever grow; a launch waits for `epoch * count`, where the epoch (launch number) is kept in
 // the workspace and advanced by the last workgroup to finish, so no counter is ever reset (the
 // workspace must be zero-filled once, before its first use).  Hand-offs are agent-scope
@@ -98,7 +101,10 @@ __device__ __forceinline__ uint32_t* counter(const MegaParams& p, int layer, int
   return p.cnt + ((size_t)layer * kNumCounters + kind) * p.nrb + rb;
 }
 
-// Block-wide: wait until *c has reached `target` (mod 2^32), bounded.
+// Block-wide: wait until *c has reached `target` (mod 2^32), bounded.  Thread 0 polls and then
+// performs the agent-scope acquire (it invalidates this CU's L1 and the XCD's L2 copies of other
+// XCDs' data for the whole workgroup); the barrier orders every other wave's later loads after
+// it.
 __device__ void mk_wait(const MegaParams& p, const uint32_t* c, uint32_t target) {
   if (threadIdx.x == 0) {
     uint32_t spins = 0;
@@ -113,14 +119,18 @@ __device__ void mk_wait(const MegaParams& p, const uint32_t* c, uint32_t target)
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 
-// Block-wide: publish this block's writes and count one arrival on *c.
+// Block-wide: publish this block's writes and count one arrival on *c.  Every wave first waits
+// for its own stores to complete; after the barrier one agent-scope release (L2 write-back of
+// the XCD) covers them all, then the counter is bumped.
 __device__ void mk_signal(uint32_t* c) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // s_waitcnt on the vector-memory counter only: at most N loads of this wave still in flight.
@@ -279,7 +289,9 @@ __device__ void mk_gemm_tile(const half* A, const half* W, int K, int row0, int 
   // lane's row, 4 x 4 features.
   const int ml = wm * 32 + frow;
   const int mrow = row0 + min(ml, nrows - 1);
-  half4 res[4];
+  half4 res[4], bv[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) bv[g] = *(const half4*)(ep.bias + n0 + wn * 32 + 8 * g + 4 * fhi);
   bool ok = true;
   if constexpr (RESID) {
     ok = ep.valid == nullptr || ep.valid[mrow] != 0;
@@ -294,11 +306,29 @@ __device__ void mk_gemm_tile(const half* A, const half* W, int K, int row0, int 
   floatx16 acc;
 #pragma unroll
   for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  auto step = [&](const half* wb, const half* abase) {
+    half8 a[4], b[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int pc = (2 * kk + fhi) ^ fx;
+      b[kk] = *(const half8*)(abase + (wm * 32 + frow) * 64 + pc * 8);
+      a[kk] = *(const half8*)(wb + (wn * 32 + frow) * 64 + pc * 8);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) acc = mfma32x32x16(a[kk], b[kk], acc);
+  };
+  if (nk <= R::NS - 1) {
+    // Every K step is already in flight: one wait and one barrier.
+    wait_vmcnt<0>();
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt)
+      step(R::w(lds, kt), RESA ? lds + kt * kMB * 64 : R::a(lds, kt));
+  }
   // Issue order of this wave's loads: W copies of the prologue steps (mk_prefetch_w), then the
-  // residual loads, then the A copies of the prologue steps, then W and A of each later step
-  // together.  Step kt is complete once at most the loads issued after its last copy are in
+  // bias / residual loads, then the A copies of the prologue steps, then W and A of each later
+  // step together.  Step kt is complete once at most the loads issued after its last copy are in
   // flight: `newer` counts those.
-  for (int kt = 0; kt < nk; ++kt) {
+  for (int kt = 0; kt < nk && nk > R::NS - 1; ++kt) {
     const int issued = min(nk, kt + R::NS - 1);  // steps whose copies are out
     int newer;
     if (RESA) newer = 2 * (issued - 1 - kt);
@@ -311,15 +341,7 @@ __device__ void mk_gemm_tile(const half* A, const half* W, int K, int row0, int 
       mk_copy_w(W, K, n0, nxt * 64, R::w(lds, nxt));
       if constexpr (!RESA) mk_copy_a(A, K, row0, nrows, nxt * 64, R::a(lds, nxt));
     }
-    const half* wb = R::w(lds, kt);
-    const half* abase = RESA ? lds + kt * kMB * 64 : R::a(lds, kt);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int pc = (2 * kk + fhi) ^ fx;
-      const half8 b = *(const half8*)(abase + (wm * 32 + frow) * 64 + pc * 8);
-      const half8 a = *(const half8*)(wb + (wn * 32 + frow) * 64 + pc * 8);
-      acc = mfma32x32x16(a, b, acc);
-    }
+    step(R::w(lds, kt), RESA ? lds + kt * kMB * 64 : R::a(lds, kt));
   }
   __syncthreads();  // the ring and the resident area are free for the next task
   // Epilogue straight from registers: acc[4g+e] = C[m][n], m = row0 + 32 wm + lane % 32,
@@ -329,11 +351,10 @@ __device__ void mk_gemm_tile(const half* A, const half* W, int K, int row0, int 
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int n = n0 + wn * 32 + 8 * g + 4 * fhi;
-    const half4 bv = *(const half4*)(ep.bias + n);
     half4 h;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float v = acc[4 * g + e] + (float)bv[e];
+      const float v = acc[4 * g + e] + (float)bv[g][e];
       if constexpr (MODE == TT_EPI_BIAS_GELU) {
         h[e] = (half)gelu_erf(v);
       } else if constexpr (RESID) {
@@ -449,12 +470,14 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
         mk_wait(p, counter(p, l, cQKV, b * p.nsb + j), epoch * (uint32_t)p.tq);
       trace_stamp(p, t, 2);
       attention_block<HD, CAUSAL>(aa, bh, qb, kv_end, prefix, sk, sv);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      if (threadIdx.x == 0)
+      if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         for (int j = 2 * qb; j < min(2 * qb + 2, p.nsb); ++j)
-          __hip_atomic_fetch_add(counter(p, l, cATT, b * p.nsb + j), 1u, __ATOMIC_RELEASE,
+          __hip_atomic_fetch_add(counter(p, l, cATT, b * p.nsb + j), 1u, __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
+      }
       trace_stamp(p, t, 3);
       continue;
     }
@@ -605,14 +628,12 @@ static int launch_mega(MegaParams& p, hipStream_t stream) {
   int dev = 0, cus = 0;
   TT_HIP(hipGetDevice(&dev));
   TT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-  // As many workgroups as the widest stage has tasks, within what can be co-resident.
+  // As many workgroups as the widest stage has tasks, at most one per CU (all resident).
   const int widest = std::max({p.nrb * p.tq, p.B * p.H * p.nqb, p.nrb * p.tf, p.nrb * p.td});
-  int grid = std::min(widest, cus * std::max(per_cu, 1));
-  grid = std::max(1, std::min(grid, cus));
-  void* args[] = {&p};
-  TT_HIP(hipLaunchCooperativeKernel((const void*)megakernel<HD, CAUSAL>, dim3(grid),
-                                    dim3(kMKThreads), args, lds, stream));
-  return TT_OK;
+  if (per_cu < 1) return fail(TT_ERR_HIP, "megakernel: a workgroup does not fit a CU");
+  const int grid = std::max(1, std::min(widest, cus));
+  hipLaunchKernelGGL((megakernel<HD, CAUSAL>), dim3(grid), dim3(kMKThreads), lds, stream, p);
+  return launch_status("megakernel");
 }
 
 int megakernel_tasks(int B, int S, int D, int H, int F, int L) {

@@ -10,7 +10,7 @@ any work, as the reference does for unsupported shapes.
 The module packs the parameter model's fp16 weights once (``prepare``) into the layout of
 ``tt_weight_layout`` and runs every forward as one call into the HIP library on the caller's
 current stream: either the layer-wise plan (LN, four GEMMs with fused epilogues and attention per
-layer) or, for small token counts, the persistent megakernel (one cooperative launch for the whole
+layer) or, for small token counts, the persistent megakernel (one launch for the whole
 stack, workgroups handing work to each other through dependency counters); ``plan`` forces one.
 It returns a fresh output tensor per call; repeated calls on the same inputs are bit-identical.
 A module instance owns one workspace per (batch, seq, plan) -- for the megakernel it holds the
