@@ -10,6 +10,7 @@ from .optimized_transformer import (
     PLAN_AUTO,
     PLAN_LAYERWISE,
     PLAN_MEGAKERNEL,
+    GraphedOptimizedTransformer,
     OptimizedTransformer,
     check_supported,
     make_optimized_transformer,
@@ -20,6 +21,7 @@ __all__ = [
     "BaselineTransformer",
     "TransformerConfig",
     "OptimizedTransformer",
+    "GraphedOptimizedTransformer",
     "make_optimized_transformer",
     "pack_model_weights",
     "check_supported",
