@@ -56,6 +56,14 @@ __device__ __forceinline__ floatx4 mfma16x16x32(half8 a, half8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// s_waitcnt on the vector-memory counter only: wait until at most N of this wave's vector memory
+// operations are still in flight (loads, including global -> LDS copies, complete in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
 // Global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane l writes LDS bytes
 // [16 l, 16 l + 16) after the wave-uniform destination `lds_dst`.
 __device__ __forceinline__ void lds_copy16(const half* src, half* lds_dst) {

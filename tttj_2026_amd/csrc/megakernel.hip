@@ -133,13 +133,6 @@ __device__ void mk_signal(uint32_t* c) {
   }
 }
 
-// s_waitcnt on the vector-memory counter only: at most N loads of this wave still in flight.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
-}
-
 // Wait until at most `newer` (even, <= 28) of this wave's loads are still in flight.
 __device__ __forceinline__ void wait_newer(int newer) {
   switch (newer >> 1) {
