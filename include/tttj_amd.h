@@ -35,7 +35,12 @@ extern "C" {
  *                         [2D,3D) -> V^T [B,H,hd,Sp] with Sp = S rounded up to a multiple of
  *                         64 (y points at Q; K and V^T follow at offsets B*S*D and 2*B*S*D
  *                         elements; the V^T region holds B*D*Sp elements).  Needs batch/seq/heads.
- * `valid` may be NULL (all rows valid).  `residual` may alias `y` (in-place update). */
+ * `valid` may be NULL (all rows valid).  With `valid`, rows whose byte is 0 are written as +0.0
+ * by TT_EPI_BIAS, TT_EPI_BIAS_GELU and TT_EPI_QKV (Q, K and V^T entries of that token), and a
+ * tile whose rows are all masked does no MMA work (it only writes those fill values).  For the
+ * non-QKV epilogues `seq` may be 0, or the rows per sequence: with `valid`, row tiles are then
+ * visited in an order that spreads each sequence's padded tail over the XCDs (results unchanged).
+ * `residual` may alias `y` (in-place update). */
 #define TT_EPI_BIAS 0
 #define TT_EPI_BIAS_GELU 1
 #define TT_EPI_RESID_MASKED 2

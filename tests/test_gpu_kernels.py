@@ -109,6 +109,86 @@ def test_linear_residual_epilogues(device, mode, m, n, k):
     assert torch.equal(r2, y)
 
 
+def _padded_rows(m, seed):
+    """Row mask with a long padded tail (whole tiles of every size masked), holes and a valid
+    last-but-one block, so fully masked, partly masked and unmasked tiles all occur."""
+    g = torch.Generator().manual_seed(seed)
+    v = torch.rand(m, generator=g) > 0.2
+    v[int(0.55 * m):] = False
+    v[m - 70:m - 40] = True
+    return v
+
+
+@pytest.mark.parametrize("tile", [-1, 2, 4])
+@pytest.mark.parametrize("mode", ["bias", "gelu", "resid_masked", "masked_resid"])
+@pytest.mark.parametrize("m,n,k,seq", [(1000, 512, 256, 0), (4096, 1024, 512, 0),
+                                       (4096, 1024, 512, 512), (8192, 256, 256, 1024)])
+def test_linear_masked_rows(device, m, n, k, seq, mode, tile):
+    """With a row mask, masked rows get the mode's fill value bitwise (+0.0, or the residual for
+    resid_masked) -- tiles of masked rows skip the MMA -- and valid rows match the reference."""
+    lib = _lib.load()
+    x = _rand((m, k), 90, 1.0)
+    w = _rand((n, k), 91, 1.0 / math.sqrt(k))
+    b = _rand((n,), 92, 0.5)
+    r = _rand((m, n), 93, 2.0)
+    if seq:   # right-padded sequences of random lengths (whole padded tiles at every tail)
+        g = torch.Generator().manual_seed(94)
+        lens = torch.randint(seq // 4, seq + 1, (m // seq,), generator=g)
+        v = (torch.arange(seq)[None, :] < lens[:, None]).reshape(-1)
+    else:
+        v = _padded_rows(m, 94)
+    vd = v.to(device)
+    branch = _linear_ref(x, w, b)
+    if mode == "gelu":
+        branch = O.gelu_erf(branch)
+    _lib.check(lib.tt_gemm_tile_override(tile), "override")
+    try:
+        if mode in ("bias", "gelu"):
+            y = ops.linear(x, w, b, mode, valid=vd, seq=seq)
+            ref = branch
+        else:
+            y = ops.linear(x, w, b, mode, residual=r, valid=vd, seq=seq)
+            ref = r.float().cpu() + branch
+        torch.cuda.synchronize()
+    finally:
+        lib.tt_gemm_tile_override(-1)
+    got = y.cpu()
+    err = (got.float()[v] - ref[v]).abs().max().item()
+    assert err <= 3e-3 * max(1.0, ref[v].abs().max().item()), err
+    if mode == "resid_masked":
+        assert torch.equal(got[~v], r.cpu()[~v])
+    else:
+        assert _bits_zero(got[~v])
+
+
+@pytest.mark.parametrize("tile", [-1, 2, 4])
+@pytest.mark.parametrize("b,s,d,h", [(4, 256, 512, 8), (3, 100, 256, 4), (2, 1024, 1024, 16)])
+def test_qkv_projection_masked_tokens(device, b, s, d, h, tile):
+    """Masked tokens get +0.0 in Q, K and V^T (whole masked tiles skip the MMA); others match."""
+    lib = _lib.load()
+    x = _rand((b, s, d), 95)
+    w = _rand((3 * d, d), 96, 1.0 / math.sqrt(d))
+    bias = _rand((3 * d,), 97, 0.5)
+    mask = _padded_rows(b * s, 98).reshape(b, s)
+    _lib.check(lib.tt_gemm_tile_override(tile), "override")
+    try:
+        q, k, vt = ops.qkv_projection(x, w, bias, h, valid=mask.to(device))
+        torch.cuda.synchronize()
+    finally:
+        lib.tt_gemm_tile_override(-1)
+    hd = d // h
+    ref = _linear_ref(x.reshape(-1, d), w, bias).reshape(b, s, 3, h, hd)
+    ref = ref * mask[:, :, None, None, None]
+    for got, want in ((q, ref[:, :, 0].permute(0, 2, 1, 3)), (k, ref[:, :, 1].permute(0, 2, 1, 3)),
+                      (vt[..., :s], ref[:, :, 2].permute(0, 2, 3, 1))):
+        err = (got.float().cpu() - want).abs().max().item()
+        assert err <= 2e-3 * max(1.0, want.abs().max().item()), err
+    qc, kc, vc = q.cpu(), k.cpu(), vt[..., :s].cpu()
+    mb = ~mask
+    assert _bits_zero(qc.permute(0, 2, 1, 3)[mb]) and _bits_zero(kc.permute(0, 2, 1, 3)[mb])
+    assert _bits_zero(vc.permute(0, 3, 1, 2)[mb])
+
+
 def test_linear_rejects_bad_shapes(device):
     x = _rand((64, 96), 1)
     w = _rand((64, 96), 2)

@@ -219,11 +219,16 @@ extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint
   const half* cur = (const half*)x;
   for (int l = 0; l < L; ++l) {
     const half* w = wts + (size_t)l * lay.stride;
-    if ((rc = launch_layernorm(cur, w + lay.off[0], w + lay.off[1], nullptr, ws.xn, T, D, 1e-5f,
+    // With a mask, padded rows are skipped from here on: LN writes them as +0.0, the QKV and
+    // ffn_in projections write +0.0 (tiles of padded rows do no MMA work), out_proj keeps the
+    // residual and ffn_out zeroes them (the block mask).  No valid token reads a padded row's
+    // values: keys with mask 0 get probability 0, and every later op is row-wise.
+    if ((rc = launch_layernorm(cur, w + lay.off[0], w + lay.off[1], mask, ws.xn, T, D, 1e-5f,
                                stream)) != TT_OK)
       return rc;
     EpiArgs ep{};
     ep.bias = w + lay.off[3];
+    ep.valid = mask;
     ep.y = q;
     ep.ldy = 3 * D;
     ep.mode = TT_EPI_QKV;
@@ -239,15 +244,18 @@ extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint
     ep.bias = w + lay.off[5];
     ep.resid = cur;
     ep.valid = mask;
+    ep.seq = S;  // row-tile balancing of padded batches
     ep.y = ws.xa;
     ep.ldy = D;
     ep.mode = TT_EPI_RESID_MASKED;
     if ((rc = launch_linear(ws.xn, w + lay.off[4], T, D, D, ep, stream)) != TT_OK) return rc;
-    if ((rc = launch_layernorm(ws.xa, w + lay.off[6], w + lay.off[7], nullptr, ws.xn, T, D, 1e-5f,
+    if ((rc = launch_layernorm(ws.xa, w + lay.off[6], w + lay.off[7], mask, ws.xn, T, D, 1e-5f,
                                stream)) != TT_OK)
       return rc;
     ep = EpiArgs{};
     ep.bias = w + lay.off[9];
+    ep.valid = mask;
+    ep.seq = S;  // row-tile balancing of padded batches
     ep.y = ws.hbuf;
     ep.ldy = F;
     ep.mode = TT_EPI_BIAS_GELU;
@@ -256,6 +264,7 @@ extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint
     ep.bias = w + lay.off[11];
     ep.resid = ws.xa;
     ep.valid = mask;
+    ep.seq = S;  // row-tile balancing of padded batches
     ep.y = ws.xa;
     ep.ldy = D;
     ep.mode = TT_EPI_MASKED_RESID;

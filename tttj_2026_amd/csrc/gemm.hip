@@ -40,6 +40,21 @@ __device__ __forceinline__ void tile_coords(int t, int tiles_m, int tiles_n, int
   tn = r / gm;
 }
 
+// Row-tile order for masked launches.  The XCD-aware mapping hands each XCD a contiguous range of
+// row tiles, which for right-padded batches is whole sequences: the XCD with the longest sequence
+// would then set the time while padded tiles elsewhere finish early.  With S a multiple of BM,
+// row tile (q, p) (sequence q, position p) is visited in diagonal order -- list index
+// L = d * nseq + q holds (q, (q + d) mod P) -- so every XCD's range mixes positions of different
+// sequences and the skipped (padded) tiles spread over all XCDs.  A bijection on [0, tiles_m).
+__device__ __forceinline__ int balance_row_tile(int tm, int tiles_m, int seq, int bm) {
+  if (seq <= 0 || seq % bm != 0) return tm;
+  const int P = seq / bm;             // row tiles per sequence
+  if (tiles_m % P != 0) return tm;
+  const int nseq = tiles_m / P;
+  const int d = tm / nseq, q = tm - d * nseq;
+  return q * P + (q + d) % P;
+}
+
 // Scalar store of 4 consecutive output features n..n+3 of row m into the QKV layout (used only
 // for the V^T part when tokens of one 8-row group may belong to two sequences, S % 8 != 0).
 __device__ __forceinline__ void store_vt4(const EpiArgs& ep, int m, int n, half4 h) {
@@ -56,6 +71,58 @@ __device__ __forceinline__ void store_vt4(const EpiArgs& ep, int m, int n, half4
 
 __device__ __forceinline__ half8 swap_halves(half8 t) {
   return half8{t[4], t[5], t[6], t[7], t[0], t[1], t[2], t[3]};
+}
+
+// Output of a tile whose rows are all padded (valid == 0): no MMA work, only the fill values the
+// epilogue would produce for masked rows -- the residual for TT_EPI_RESID_MASKED (the masked
+// branch adds nothing), +0.0 for every other mode.  16-byte stores over the tile's BM x BN block
+// (for the V part of the QKV projection: V^T rows, 8 tokens at a time when they share a sequence).
+template <int BM, int BN, int MODE>
+__device__ void fill_padded_tile(const EpiArgs& ep, int M, int m0, int n0) {
+  constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  if constexpr (MODE == TT_EPI_QKV) {
+    const int D = ep.d_model, hd = ep.head_dim, S = ep.seq;
+    const size_t plane = (size_t)ep.batch * S * D;
+    if (n0 < 2 * D) {  // Q or K rows: 8 features of one head of token m per chunk
+      for (int e = threadIdx.x; e < BM * CPR; e += blockDim.x) {
+        const int m = m0 + e / CPR, n = n0 + 8 * (e % CPR);
+        if (m >= M) continue;
+        const int which = n / D, nn = n - which * D;
+        const int hh = nn / hd, d = nn - hh * hd;
+        const int bb = m / S, sq = m - bb * S;
+        *(u32x4*)(ep.y + which * plane + (((size_t)bb * ep.heads + hh) * S + sq) * hd + d) = zero;
+      }
+    } else {           // V^T: feature row n, tokens m .. m + 7
+      const size_t ldv = (size_t)(S + 63) / 64 * 64;
+      for (int e = threadIdx.x; e < BN * (BM / 8); e += blockDim.x) {
+        const int n = n0 + e / (BM / 8), m = m0 + 8 * (e % (BM / 8));
+        const int nn = n - 2 * D, hh = nn / hd, d = nn - hh * hd;
+        half* row = ep.y + 2 * plane + ((size_t)hh * hd + d) * ldv;
+        const int bb = m / S, sq = m - bb * S;
+        if (S % 8 == 0 && m + 8 <= M) {
+          *(u32x4*)(row + (size_t)bb * ep.heads * hd * ldv + sq) = zero;
+        } else {
+          for (int t = m; t < min(m + 8, M); ++t) {
+            const int b2 = t / S, s2 = t - b2 * S;
+            row[(size_t)b2 * ep.heads * hd * ldv + s2] = (half)0.f;
+          }
+        }
+      }
+    }
+  } else {
+    for (int e = threadIdx.x; e < BM * CPR; e += blockDim.x) {
+      const int m = m0 + e / CPR, c = 8 * (e % CPR);
+      if (m >= M) continue;
+      half* dst = ep.y + (size_t)m * ep.ldy + n0 + c;
+      if constexpr (MODE == TT_EPI_RESID_MASKED) {
+        const half* src = ep.resid + (size_t)m * ep.ldy + n0 + c;
+        if (src != dst) *(u32x4*)dst = *(const u32x4*)src;
+      } else {
+        *(u32x4*)dst = zero;
+      }
+    }
+  }
 }
 
 // LDS tile of R rows x 64 halfs (128-byte rows) holding a K slice of one operand.  Global ->
@@ -84,10 +151,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
   const int tiles_m = (M + BM - 1) / BM, tiles_n = N / BN;
   int tm, tn;
   tile_coords(xcd_remap(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
+  if (ep.valid != nullptr) tm = balance_row_tile(tm, tiles_m, ep.seq, BM);
   const int m0 = tm * BM, n0 = tn * BN;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wn = wave & 1, wm = wave >> 1;
+
+  // Padded-row skip: with a row mask, a tile whose rows are all padded (e.g. the tail of a
+  // right-padded sequence) does no MMA work.
+  if (ep.valid != nullptr) {
+    int v = 0;
+    if ((int)threadIdx.x < BM && m0 + (int)threadIdx.x < M) v = ep.valid[m0 + threadIdx.x];
+    if (!__syncthreads_or(v)) {
+      fill_padded_tile<BM, BN, MODE>(ep, M, m0, n0);
+      return;
+    }
+  }
 
   // Copy sources: copy i of this wave fills 8-row group wave + 4 i of the stage.  X rows past M
   // are clamped to M - 1 (valid memory whose results are never stored).
@@ -204,9 +283,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
     vt_mode = n0 >= 2 * ep.d_model;   // tiles never straddle the Q / K / V boundaries
     vt_scalar = vt_mode && (ep.seq % 8 != 0);
   }
+  // Modes without a residual write masked rows as +0.0 (the residual modes handle the mask
+  // when they store).
+  constexpr bool ZERO_MASKED = MODE == TT_EPI_BIAS || MODE == TT_EPI_BIAS_GELU || MODE == TT_EPI_QKV;
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
     const int ml = j * 32 + (lane & 31);
+    bool keep = true;
+    if constexpr (ZERO_MASKED) keep = ep.valid == nullptr || ep.valid[min(mw + ml, M - 1)] != 0;
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
 #pragma unroll
@@ -218,7 +302,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
         for (int e = 0; e < 4; ++e) {
           float v = acc[i][j][4 * g + e] + (float)bv[e];
           if constexpr (MODE == TT_EPI_BIAS_GELU) v = gelu_erf(v);
-          h[e] = (half)v;
+          h[e] = keep ? (half)v : (half)0.f;
         }
         if (vt_scalar) {
           if (mw + ml < M) store_vt4(ep, mw + ml, nw + nl, h);

@@ -52,8 +52,9 @@ def layernorm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, epilogue: str = "bias",
            residual: Optional[torch.Tensor] = None, valid: Optional[torch.Tensor] = None,
-           out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """``epilogue`` in {"bias", "gelu", "resid_masked", "masked_resid"} (see tt_linear_fwd)."""
+           out: Optional[torch.Tensor] = None, seq: int = 0) -> torch.Tensor:
+    """``epilogue`` in {"bias", "gelu", "resid_masked", "masked_resid"} (see tt_linear_fwd).
+    ``seq`` (rows per sequence, with ``valid``) only changes the order tiles are visited in."""
     if epilogue not in ("bias", "gelu", "resid_masked", "masked_resid"):
         raise ValueError(f"unknown epilogue {epilogue!r}")
     x = _half(x, "x")
@@ -71,22 +72,25 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, epilogue: 
     y = out if out is not None else torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=x.device)
     rc = _lib.load().tt_linear_fwd(x.data_ptr(), weight.data_ptr(), _half(bias, "bias").data_ptr(),
                                    _ptr(residual), _ptr(valid), y.data_ptr(), m, n, k,
-                                   _lib.EPILOGUES[epilogue], 0, 0, 0, _stream(x))
+                                   _lib.EPILOGUES[epilogue], 0, int(seq), 0, _stream(x))
     _lib.check(rc, "tt_linear_fwd")
     return y
 
 
 def qkv_projection(x: torch.Tensor, wqkv: torch.Tensor, bqkv: torch.Tensor,
-                   heads: int) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """x [B,S,D] -> (q [B,H,S,hd], k [B,H,S,hd], vt [B,H,hd,Sp]) with Sp = S rounded up to 64."""
+                   heads: int, valid: Optional[torch.Tensor] = None
+                   ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """x [B,S,D] -> (q [B,H,S,hd], k [B,H,S,hd], vt [B,H,hd,Sp]) with Sp = S rounded up to 64.
+    With ``valid`` ([B,S] bool), tokens whose mask is False get +0.0 in q, k and vt."""
     x = _half(x, "x")
     b, s, d = x.shape
+    valid = _mask(valid, b * s)
     hd = d // heads
     sp = (s + 63) // 64 * 64
     plane = b * s * d
     buf = torch.empty(2 * plane + b * d * sp, dtype=torch.float16, device=x.device)
     rc = _lib.load().tt_linear_fwd(x.data_ptr(), _half(wqkv, "wqkv").data_ptr(),
-                                   _half(bqkv, "bqkv").data_ptr(), None, None, buf.data_ptr(),
+                                   _half(bqkv, "bqkv").data_ptr(), None, _ptr(valid), buf.data_ptr(),
                                    b * s, 3 * d, d, _lib.EPILOGUES["qkv"], b, s, heads,
                                    _stream(x))
     _lib.check(rc, "tt_linear_fwd(qkv)")
