@@ -8,6 +8,7 @@ loaded with ctypes; PyTorch-ROCm provides device memory and streams.
 from .model import BaselineTransformer, TransformerConfig
 from .optimized_transformer import (
     PLAN_AUTO,
+    PLAN_FUSED_LN,
     PLAN_LAYERWISE,
     PLAN_MEGAKERNEL,
     GraphedOptimizedTransformer,
@@ -28,4 +29,5 @@ __all__ = [
     "PLAN_AUTO",
     "PLAN_LAYERWISE",
     "PLAN_MEGAKERNEL",
+    "PLAN_FUSED_LN",
 ]

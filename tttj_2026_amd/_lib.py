@@ -14,7 +14,7 @@ import threading
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libtttj_amd.so"
 
 TT_OK, TT_ERR_INVALID, TT_ERR_HIP = 0, 1, 2
-PLAN_AUTO, PLAN_LAYERWISE, PLAN_MEGAKERNEL = 0, 1, 2
+PLAN_AUTO, PLAN_LAYERWISE, PLAN_MEGAKERNEL, PLAN_FUSED_LN = 0, 1, 2, 3
 EPILOGUES = {"bias": 0, "gelu": 1, "resid_masked": 2, "masked_resid": 3, "qkv": 4}
 
 _P = ctypes.c_void_p

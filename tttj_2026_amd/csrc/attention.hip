@@ -7,8 +7,12 @@ namespace tt {
 
 template <int HD, bool CAUSAL>
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a, const int32_t* __restrict__ info) {
-  __shared__ __align__(16) half sk[2 * kBKV * HD];
-  __shared__ __align__(16) half sv[2 * HD * kBKV];
+  // Dynamic LDS: with statically declared tiles the compiler makes the first K-fragment read of
+  // every tile wait (vmcnt(0)) for the next tile's in-flight global -> LDS copies, serialising
+  // the prefetch; from the dynamic area it relies on the explicit waits, as intended.
+  extern __shared__ __align__(16) half att_lds[];
+  half* sk = att_lds;
+  half* sv = att_lds + 2 * kBKV * HD;
   const int BH = a.B * a.H;
   const int nqt = (a.S + kBQ - 1) / kBQ;
   const int bh = blockIdx.x % BH;
@@ -77,8 +81,9 @@ int launch_attention(const half* q, const half* k, const half* vt, const uint8_t
   const float scale_log2 = (1.0f / sqrtf((float)head_dim)) * 1.4426950408889634f;
   const dim3 grid((unsigned)blocks), block(256);
   const AttnArgs args{q, k, vt, mask, ctx, batch, seq, heads, scale_log2};
-#define TT_ATT(HD, C) \
-  hipLaunchKernelGGL((attention_kernel<HD, C>), grid, block, 0, stream, args, info)
+#define TT_ATT(HD, C)                                                                          \
+  hipLaunchKernelGGL((attention_kernel<HD, C>), grid, block, 4 * kBKV * HD * sizeof(half), stream, \
+                     args, info)
   if (head_dim == 64) {
     if (causal) TT_ATT(64, true); else TT_ATT(64, false);
   } else {

@@ -162,8 +162,18 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
   float m_ref = -INFINITY;  // reference max (log2 domain) the running sums are scaled to
   float l_run = 0.f;        // this lane's half of the row sum
 
+  // Non-prefix masks: this lane's key-mask byte for the current and the next tile, loaded when
+  // the tile's copies are issued so the end-of-tile wait covers it.
+  // The raw byte is kept (address clamped, bound applied at use) so the load's wait lands at the
+  // use, not at the load.
+  auto mask_byte = [&](int t0) -> int {
+    const int key = min(t0 + lane, S - 1);
+    return mask[(size_t)b * S + key];
+  };
+  int mcur = 0, mnext = 0;
   if (ntiles > 0) {
     issue_tile(0, 0);
+    if (keymask) mcur = mask_byte(0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (kBKV > S) {
@@ -174,7 +184,10 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
   for (int t = 0; t < ntiles; ++t) {
     const int st = t & 1;
     const int t0 = t * kBKV;
-    if (t + 1 < ntiles) issue_tile(t0 + kBKV, st ^ 1);
+    if (t + 1 < ntiles) {
+      issue_tile(t0 + kBKV, st ^ 1);
+      if (keymask) mnext = mask_byte(t0 + kBKV);
+    }
     if (wave_active && t0 < wave_end) {
       floatx16 s[2];
 #pragma unroll
@@ -202,8 +215,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
           allowed |= ((1u << n) - 1u) << (8 * g);
         }
         if (keymask) {
-          const int key = t0 + lane;
-          const uint64_t kbits = __ballot(key < S && mask[(size_t)b * S + key] != 0);
+          const uint64_t kbits = __ballot(mcur != 0 && t0 + lane < S);
           allowed &= __builtin_amdgcn_perm((uint32_t)(kbits >> 32), (uint32_t)kbits,
                                            hf ? 0x07050301u : 0x06040200u);
         }
@@ -257,6 +269,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
           }
       }
     }
+    mcur = mnext;
     if (t + 1 < ntiles) {
       __builtin_amdgcn_s_waitcnt(0);  // the next tile's copies have landed ...
       __syncthreads();                // ... and every wave is done with this one

@@ -119,11 +119,17 @@ extern "C" int tt_weight_layout(int d_model, int ffn_dim, int num_layers,
 // everywhere until that changes; the megakernel is selected explicitly with TT_PLAN_MEGAKERNEL.
 static constexpr int64_t kMegaMaxTokens = 0;
 static constexpr int kMegaMaxDModel = 512;  // the megakernel keeps a LayerNorm'd 64 x D tile in LDS
+// Token count up to which the automatic plan computes LN1 / LN2 inside the QKV / ffn_in tiles
+// (fewer launches on the latency-bound path; beyond it the 64 x 64 tiles lose to the layer-wise
+// GEMM tiles).
+static constexpr int64_t kFusedLnMaxTokens = 1024;
 
 static int resolve_plan(int plan, int B, int S, int D) {
   if (plan != TT_PLAN_AUTO) return plan;
-  return ((int64_t)B * S <= kMegaMaxTokens && D <= kMegaMaxDModel) ? TT_PLAN_MEGAKERNEL
-                                                                    : TT_PLAN_LAYERWISE;
+  const int64_t T = (int64_t)B * S;
+  if (T <= kMegaMaxTokens && D <= kMegaMaxDModel) return TT_PLAN_MEGAKERNEL;
+  if (T <= kFusedLnMaxTokens && D <= kMegaMaxDModel) return TT_PLAN_FUSED_LN;
+  return TT_PLAN_LAYERWISE;
 }
 
 extern "C" int tt_workspace_bytes(int batch, int seq, int d_model, int num_heads, int ffn_dim,
@@ -131,7 +137,7 @@ extern "C" int tt_workspace_bytes(int batch, int seq, int d_model, int num_heads
   int rc = check_model_shape(batch, seq, d_model, num_heads, ffn_dim, num_layers);
   if (rc != TT_OK) return rc;
   TT_REQUIRE(bytes != nullptr, "workspace_bytes: null output");
-  TT_REQUIRE(plan >= TT_PLAN_AUTO && plan <= TT_PLAN_MEGAKERNEL, "workspace_bytes: bad plan %d", plan);
+  TT_REQUIRE(plan >= TT_PLAN_AUTO && plan <= TT_PLAN_FUSED_LN, "workspace_bytes: bad plan %d", plan);
   plan = resolve_plan(plan, batch, seq, d_model);
   if (plan == TT_PLAN_MEGAKERNEL) {
     if ((rc = megakernel_supported(batch, seq, d_model, num_heads, ffn_dim, num_layers)) != TT_OK)
@@ -144,7 +150,7 @@ extern "C" int tt_workspace_bytes(int batch, int seq, int d_model, int num_heads
 }
 
 extern "C" int tt_resolve_plan(int batch, int seq, int d_model, int plan) {
-  if (plan < TT_PLAN_AUTO || plan > TT_PLAN_MEGAKERNEL || batch <= 0 || seq <= 0 || d_model <= 0) {
+  if (plan < TT_PLAN_AUTO || plan > TT_PLAN_FUSED_LN || batch <= 0 || seq <= 0 || d_model <= 0) {
     fail(TT_ERR_INVALID, "resolve_plan: bad arguments (batch=%d seq=%d d_model=%d plan=%d)",
          batch, seq, d_model, plan);
     return -1;
@@ -192,7 +198,7 @@ extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint
   if (rc != TT_OK) return rc;
   TT_REQUIRE(weights && x && y && workspace, "transformer: null pointer");
   TT_REQUIRE(x != y, "transformer: y must not alias x");
-  TT_REQUIRE(plan >= TT_PLAN_AUTO && plan <= TT_PLAN_MEGAKERNEL, "transformer: bad plan %d", plan);
+  TT_REQUIRE(plan >= TT_PLAN_AUTO && plan <= TT_PLAN_FUSED_LN, "transformer: bad plan %d", plan);
   const int B = batch, S = seq, D = d_model, H = num_heads, F = ffn_dim, L = num_layers;
   const int T = B * S, hd = D / H;
   if (resolve_plan(plan, B, S, D) == TT_PLAN_MEGAKERNEL) {
@@ -216,6 +222,10 @@ extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint
     if ((rc = launch_mask_info(mask, ws.info, B, S, stream)) != TT_OK) return rc;
     info = ws.info;
   }
+  // TT_PLAN_FUSED_LN: LN1 / LN2 are computed inside the QKV / ffn_in tiles (launch_ln_tile), five
+  // launches per layer instead of seven.
+  const bool fused_ln = resolve_plan(plan, B, S, D) == TT_PLAN_FUSED_LN;
+  if (fused_ln && (rc = ln_tile_supported(D, F)) != TT_OK) return rc;
   const half* cur = (const half*)x;
   for (int l = 0; l < L; ++l) {
     const half* w = wts + (size_t)l * lay.stride;
@@ -223,12 +233,8 @@ extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint
     // ffn_in projections write +0.0 (tiles of padded rows do no MMA work), out_proj keeps the
     // residual and ffn_out zeroes them (the block mask).  No valid token reads a padded row's
     // values: keys with mask 0 get probability 0, and every later op is row-wise.
-    if ((rc = launch_layernorm(cur, w + lay.off[0], w + lay.off[1], mask, ws.xn, T, D, 1e-5f,
-                               stream)) != TT_OK)
-      return rc;
     EpiArgs ep{};
     ep.bias = w + lay.off[3];
-    ep.valid = mask;
     ep.y = q;
     ep.ldy = 3 * D;
     ep.mode = TT_EPI_QKV;
@@ -237,7 +243,17 @@ extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint
     ep.heads = H;
     ep.head_dim = hd;
     ep.d_model = D;
-    if ((rc = launch_linear(ws.xn, w + lay.off[2], T, 3 * D, D, ep, stream)) != TT_OK) return rc;
+    if (fused_ln) {
+      if ((rc = launch_ln_tile(cur, w + lay.off[0], w + lay.off[1], w + lay.off[2], ep, B, S, D,
+                               3 * D, stream)) != TT_OK)
+        return rc;
+    } else {
+      if ((rc = launch_layernorm(cur, w + lay.off[0], w + lay.off[1], mask, ws.xn, T, D, 1e-5f,
+                                 stream)) != TT_OK)
+        return rc;
+      ep.valid = mask;
+      if ((rc = launch_linear(ws.xn, w + lay.off[2], T, 3 * D, D, ep, stream)) != TT_OK) return rc;
+    }
     if ((rc = launch_attention(q, k, vt, mask, info, ws.xn, B, S, H, hd, causal, stream)) != TT_OK)
       return rc;
     ep = EpiArgs{};
@@ -249,17 +265,23 @@ extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint
     ep.ldy = D;
     ep.mode = TT_EPI_RESID_MASKED;
     if ((rc = launch_linear(ws.xn, w + lay.off[4], T, D, D, ep, stream)) != TT_OK) return rc;
-    if ((rc = launch_layernorm(ws.xa, w + lay.off[6], w + lay.off[7], mask, ws.xn, T, D, 1e-5f,
-                               stream)) != TT_OK)
-      return rc;
     ep = EpiArgs{};
     ep.bias = w + lay.off[9];
-    ep.valid = mask;
-    ep.seq = S;  // row-tile balancing of padded batches
     ep.y = ws.hbuf;
     ep.ldy = F;
     ep.mode = TT_EPI_BIAS_GELU;
-    if ((rc = launch_linear(ws.xn, w + lay.off[8], T, F, D, ep, stream)) != TT_OK) return rc;
+    if (fused_ln) {
+      if ((rc = launch_ln_tile(ws.xa, w + lay.off[6], w + lay.off[7], w + lay.off[8], ep, B, S, D,
+                               F, stream)) != TT_OK)
+        return rc;
+    } else {
+      if ((rc = launch_layernorm(ws.xa, w + lay.off[6], w + lay.off[7], mask, ws.xn, T, D, 1e-5f,
+                                 stream)) != TT_OK)
+        return rc;
+      ep.valid = mask;
+      ep.seq = S;  // row-tile balancing of padded batches
+      if ((rc = launch_linear(ws.xn, w + lay.off[8], T, F, D, ep, stream)) != TT_OK) return rc;
+    }
     ep = EpiArgs{};
     ep.bias = w + lay.off[11];
     ep.resid = ws.xa;

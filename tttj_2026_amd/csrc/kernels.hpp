@@ -39,4 +39,10 @@ int megakernel_tasks(int B, int S, int D, int H, int F, int L);
 int megakernel_status(const char* workspace, int B, int S, int D, int F, int L, int* status,
                       hipStream_t stream);
 
+// LayerNorm-prologue GEMM tiles (megakernel.hip): Y = LN(x) W^T + b for 64 x 64 tiles with the
+// TT_EPI_QKV or TT_EPI_BIAS_GELU epilogue, D <= 512.
+int ln_tile_supported(int D, int N);
+int launch_ln_tile(const half* x, const half* gamma, const half* beta, const half* w,
+                   const EpiArgs& ep, int B, int S, int D, int N, hipStream_t stream);
+
 }  // namespace tt

@@ -160,9 +160,14 @@ static_assert(2 * (kRingW - 1) <= 28 && 4 * (kRingAW - 2) <= 28, "wait_newer ran
 // OUT_LDS: write the normalised rows [0, 64) into the resident A area of LDS as
 // [D/64][64 rows][64 halfs] with 16-byte chunks swizzled by row (rows past nrows are zero);
 // otherwise write rows [0, nrows) to dst (global, row stride D), as +0.0 where the mask is 0.
-template <int G, bool OUT_LDS>
+struct NoHook {
+  __device__ void operator()() const {}
+};
+
+template <int G, bool OUT_LDS, typename Hook = NoHook>
 __device__ void mk_layernorm_block(const half* src, const half* gamma, const half* beta,
-                                   const uint8_t* valid, int row0, int nrows, int D, half* dst) {
+                                   const uint8_t* valid, int row0, int nrows, int D, half* dst,
+                                   Hook hook = Hook{}) {
   constexpr int RPP = 64 / G;                 // rows per wave pass
   constexpr int PASSES = kMB / (4 * RPP);     // passes per wave (4 waves cover the 64 rows)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -181,6 +186,7 @@ __device__ void mk_layernorm_block(const half* src, const half* gamma, const hal
     v[i] = half8{};
     if (act && r < nrows) v[i] = *(const half8*)(src + (size_t)(row0 + r) * D + 8 * c);
   }
+  hook();  // issued after the row loads, so the reductions below do not wait for its loads
 #pragma unroll
   for (int i = 0; i < PASSES; ++i) {
     const int r = (i * 4 + wave) * RPP + lane / G;
@@ -212,14 +218,15 @@ __device__ void mk_layernorm_block(const half* src, const half* gamma, const hal
   }
 }
 
-template <bool OUT_LDS>
+template <bool OUT_LDS, typename Hook = NoHook>
 __device__ void mk_layernorm(const half* src, const half* gamma, const half* beta,
-                             const uint8_t* valid, int row0, int nrows, int D, half* dst) {
+                             const uint8_t* valid, int row0, int nrows, int D, half* dst,
+                             Hook hook = Hook{}) {
   const int nch = D >> 3;
-  if (nch <= 8) mk_layernorm_block<8, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst);
-  else if (nch <= 16) mk_layernorm_block<16, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst);
-  else if (nch <= 32) mk_layernorm_block<32, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst);
-  else mk_layernorm_block<64, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst);
+  if (nch <= 8) mk_layernorm_block<8, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst, hook);
+  else if (nch <= 16) mk_layernorm_block<16, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst, hook);
+  else if (nch <= 32) mk_layernorm_block<32, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst, hook);
+  else mk_layernorm_block<64, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst, hook);
 }
 
 // ---- 64 x 64 GEMM tile, K streamed through an LDS ring of K steps ----
@@ -409,6 +416,37 @@ __device__ void mk_mask_summary(const MegaParams& p, int b, int* sred, int& kv_e
   __syncthreads();
   kv_end = last + 1;
   prefix = count == last + 1;
+}
+
+// ---- Standalone LayerNorm-prologue GEMM tiles (layer-wise plan for few tokens) ----
+// Block (rb, nt): LayerNorm of the 64-row block rb (gamma, beta) straight into LDS, then the
+// 64-column tile nt of Y = LN(X) W^T + b with epilogue MODE (TT_EPI_QKV or TT_EPI_BIAS_GELU).
+// Replaces a LayerNorm launch + a GEMM launch: the norm is recomputed by each column tile of
+// the row block (D <= kMaxD), which costs a few microseconds of VALU less than a separate
+// launch and its global round trip when the launches themselves are the critical path.
+struct LnTileArgs {
+  const half* x;      // [B * S, D] rows to normalise
+  const half* gamma;
+  const half* beta;
+  const half* w;      // [N, D]
+  EpiArgs ep;         // bias, output and the QKV layout fields
+  int S, D, N;
+};
+
+template <int MODE>
+__global__ __launch_bounds__(kMKThreads) void ln_tile_kernel(LnTileArgs a) {
+  extern __shared__ __align__(16) half lds[];
+  const int nsb = (a.S + kMB - 1) / kMB;
+  const int tiles = a.N / kNB;
+  const int rb = blockIdx.x / tiles, nt = blockIdx.x - rb * tiles;
+  const int b = rb / nsb, sb = rb - b * nsb;
+  const int row0 = b * a.S + sb * kMB, nrows = min(kMB, a.S - sb * kMB);
+  const int n0 = nt * kNB;
+  // Row loads first, then the weight prefetch, then the reductions: the norm waits only for the
+  // rows, and the weights stream in meanwhile.
+  mk_layernorm<true>(a.x, a.gamma, a.beta, nullptr, row0, nrows, a.D, lds,
+                     [&] { mk_prefetch_w<true>(a.w, a.D, n0, lds); });
+  mk_gemm_tile<MODE, true>(nullptr, a.w, a.D, row0, nrows, n0, a.ep, lds);
 }
 
 template <int HD, bool CAUSAL>
@@ -627,6 +665,39 @@ static int launch_mega(MegaParams& p, hipStream_t stream) {
   const int grid = std::max(1, std::min(widest, cus));
   hipLaunchKernelGGL((megakernel<HD, CAUSAL>), dim3(grid), dim3(kMKThreads), lds, stream, p);
   return launch_status("megakernel");
+}
+
+template <int MODE>
+static int launch_ln_tile_mode(const LnTileArgs& a, int blocks, hipStream_t stream) {
+  const size_t lds = kLdsHalfs * sizeof(half) + 64;
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [&] {
+    attr = hipFuncSetAttribute((const void*)ln_tile_kernel<MODE>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  });
+  if (attr != hipSuccess) return fail(TT_ERR_HIP, "ln_tile setup: %s", hipGetErrorString(attr));
+  hipLaunchKernelGGL((ln_tile_kernel<MODE>), dim3(blocks), dim3(kMKThreads), lds, stream, a);
+  return launch_status("ln_tile_kernel");
+}
+
+int ln_tile_supported(int D, int N) {
+  TT_REQUIRE(D % 64 == 0 && D <= kMaxD, "ln_tile: d_model %d must be a multiple of 64 and <= %d",
+             D, kMaxD);
+  TT_REQUIRE(N % kNB == 0, "ln_tile: N %d must be a multiple of %d", N, kNB);
+  return TT_OK;
+}
+
+int launch_ln_tile(const half* x, const half* gamma, const half* beta, const half* w,
+                   const EpiArgs& ep, int B, int S, int D, int N, hipStream_t stream) {
+  int rc = ln_tile_supported(D, N);
+  if (rc != TT_OK) return rc;
+  TT_REQUIRE(ep.mode == TT_EPI_QKV || ep.mode == TT_EPI_BIAS_GELU,
+             "ln_tile: epilogue %d not supported", ep.mode);
+  LnTileArgs a{x, gamma, beta, w, ep, S, D, N};
+  const int blocks = B * ((S + kMB - 1) / kMB) * (N / kNB);
+  if (ep.mode == TT_EPI_QKV) return launch_ln_tile_mode<TT_EPI_QKV>(a, blocks, stream);
+  return launch_ln_tile_mode<TT_EPI_BIAS_GELU>(a, blocks, stream);
 }
 
 int megakernel_tasks(int B, int S, int D, int H, int F, int L) {

@@ -29,7 +29,8 @@ import torch.nn as nn
 
 from . import _lib
 
-PLAN_AUTO, PLAN_LAYERWISE, PLAN_MEGAKERNEL = _lib.PLAN_AUTO, _lib.PLAN_LAYERWISE, _lib.PLAN_MEGAKERNEL
+PLAN_AUTO, PLAN_LAYERWISE, PLAN_MEGAKERNEL, PLAN_FUSED_LN = (
+    _lib.PLAN_AUTO, _lib.PLAN_LAYERWISE, _lib.PLAN_MEGAKERNEL, _lib.PLAN_FUSED_LN)
 
 
 def check_supported(config) -> None:
@@ -107,7 +108,7 @@ class OptimizedTransformer(nn.Module):
 
     def __init__(self, parameter_model: nn.Module, plan: int = PLAN_AUTO) -> None:
         super().__init__()
-        if plan not in (PLAN_AUTO, PLAN_LAYERWISE, PLAN_MEGAKERNEL):
+        if plan not in (PLAN_AUTO, PLAN_LAYERWISE, PLAN_MEGAKERNEL, PLAN_FUSED_LN):
             raise ValueError(f"unknown plan {plan}")
         self.parameter_model = parameter_model
         self.config = parameter_model.config
