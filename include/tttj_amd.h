@@ -86,9 +86,9 @@ int tt_weight_layout(int d_model, int ffn_dim, int num_layers, int64_t layer_off
 int tt_workspace_bytes(int batch, int seq, int d_model, int num_heads, int ffn_dim, int num_layers,
                        int plan, int64_t* bytes);
 
-/* The plan TT_PLAN_AUTO resolves to for this shape (plan returned unchanged otherwise); < 0 on
- * bad arguments.  Replaces the case dispatch of optimized_transformer.py:45-93. */
-int tt_resolve_plan(int batch, int seq, int d_model, int plan);
+/* The plan TT_PLAN_AUTO resolves to for this shape (plan returned unchanged otherwise; AUTO
+ * only picks a fused plan for shapes its kernels take); < 0 on bad arguments.  Replaces the case dispatch of optimized_transformer.py:45-93. */
+int tt_resolve_plan(int batch, int seq, int d_model, int num_heads, int ffn_dim, int plan);
 
 /* Health word of a megakernel workspace (synchronises `stream`): *status = 0 when every
  * dependency wait of every launch so far completed, 1 if some wait exceeded its bound (the
@@ -120,8 +120,9 @@ int tt_layernorm_fwd(const void* x, const void* gamma, const void* beta, const u
                      void* y, int rows, int d, float eps, void* stream);
 
 /* Y[M,N] = X[M,K] W[N,K]^T + b with one of the TT_EPI_* epilogues; fp16 in/out, fp32 accumulate
- * on MFMA.  K % 64 == 0, N % 64 == 0.  For TT_EPI_QKV, N == 3*D with D = heads*head_dim and
- * M == batch*seq.  Replaces _linear_tile with EPILOGUE 0-3 (kernels/fused_megakernel.py:447-541),
+ * on MFMA when K % 64 == 0 and N % 64 == 0, else (N, K multiples of 8, e.g. d_model 32) on a
+ * small vector-ALU kernel with the same epilogues.  M * K may exceed 2^31; N * K may not.  For
+ * TT_EPI_QKV, N == 3*D with D = heads*head_dim and M == batch*seq.  Replaces _linear_tile with EPILOGUE 0-3 (kernels/fused_megakernel.py:447-541),
  * linear_gelu (kernels/case13_linear.py:149-176), the packed-QKV F.linear
  * (kernels/layerwise_hybrid.py:188-192) and _head_major_qkv_kernel (case13_linear.py:114-146). */
 int tt_linear_fwd(const void* x, const void* w, const void* bias, const void* residual,
@@ -142,7 +143,8 @@ int tt_mask_info(const uint8_t* mask, int32_t* info, int batch, int seq, void* s
 
 /* Flash attention over the TT_EPI_QKV layout: q, k [B,H,S,hd], vt [B,H,hd,Sp] -> ctx [B,S,H*hd]
  * token-major.  softmax(q k^T * hd^-0.5) with keys masked when (causal && key > query) or
- * mask[b,key] == 0; padded query rows are written as +0.0.  hd in {32, 64}.  `info` is the
+ * mask[b,key] == 0; padded query rows are written as +0.0.  hd in {8, 16, 32, 64, 128, 256}
+ * (8 / 16 on the vector ALUs with fp32 probabilities, the others on MFMA).  `info` is the
  * tt_mask_info output for the same mask (may be NULL only if mask is NULL).  Replaces
  * _attention_mxhd (kernels/fused_megakernel.py:544-790) and packed_causal_attention
  * (kernels/case8_attention.py:48-206), and BaselineSelfAttention's score/softmax/PV

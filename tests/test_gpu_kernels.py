@@ -50,7 +50,8 @@ def _linear_ref(x, w, b):
 
 
 GEMM_SHAPES = [(64, 768, 256), (100, 64, 64), (512, 1024, 256), (4096, 1536, 512),
-               (8192, 1024, 4096), (1, 128, 128), (300, 3072, 1024)]
+               (8192, 1024, 4096), (1, 128, 128), (300, 3072, 1024), (200, 512, 64),
+               (130, 256, 192)]
 
 
 @pytest.mark.parametrize("tile", [-1, 0, 1, 2, 3, 4])
@@ -119,7 +120,7 @@ def _padded_rows(m, seed):
     return v
 
 
-@pytest.mark.parametrize("tile", [-1, 2, 4])
+@pytest.mark.parametrize("tile", [-1, 0, 2, 4])
 @pytest.mark.parametrize("mode", ["bias", "gelu", "resid_masked", "masked_resid"])
 @pytest.mark.parametrize("m,n,k,seq", [(1000, 512, 256, 0), (4096, 1024, 512, 0),
                                        (4096, 1024, 512, 512), (8192, 256, 256, 1024)])
@@ -161,8 +162,10 @@ def test_linear_masked_rows(device, m, n, k, seq, mode, tile):
         assert _bits_zero(got[~v])
 
 
-@pytest.mark.parametrize("tile", [-1, 2, 4])
-@pytest.mark.parametrize("b,s,d,h", [(4, 256, 512, 8), (3, 100, 256, 4), (2, 1024, 1024, 16)])
+@pytest.mark.parametrize("tile", [-1, 0, 2, 4])
+@pytest.mark.parametrize("b,s,d,h", [(4, 256, 512, 8), (3, 100, 256, 4), (2, 1024, 1024, 16),
+                                     (4, 100, 32, 4), (2, 130, 96, 3), (3, 128, 128, 16),
+                                     (2, 64, 1024, 4), (2, 72, 128, 1)])
 def test_qkv_projection_masked_tokens(device, b, s, d, h, tile):
     """Masked tokens get +0.0 in Q, K and V^T (whole masked tiles skip the MMA); others match."""
     lib = _lib.load()
@@ -190,15 +193,49 @@ def test_qkv_projection_masked_tokens(device, b, s, d, h, tile):
 
 
 def test_linear_rejects_bad_shapes(device):
-    x = _rand((64, 96), 1)
-    w = _rand((64, 96), 2)
+    x = _rand((64, 100), 1)
+    w = _rand((64, 100), 2)
     b = _rand((64,), 3)
     with pytest.raises(ValueError):
-        ops.linear(x, w, b)  # K = 96 is not a multiple of 64
+        ops.linear(x, w, b)  # K = 100 is not a multiple of 8
     x = _rand((64, 64), 1)
-    w = _rand((96, 64), 2)
+    w = _rand((36, 64), 2)
     with pytest.raises(ValueError):
-        ops.linear(x, w, _rand((96,), 3))  # N = 96 is not a multiple of 64
+        ops.linear(x, w, _rand((36,), 3))  # N = 36 is not a multiple of 8
+
+
+@pytest.mark.parametrize("mode", ["bias", "gelu", "resid_masked", "masked_resid"])
+@pytest.mark.parametrize("m,n,k", [(1000, 96, 32), (37, 32, 32), (513, 40, 24), (256, 136, 200),
+                                   (4096, 32, 96), (64, 64, 8)])
+@pytest.mark.parametrize("masked", [False, True])
+def test_linear_small_shapes(device, m, n, k, mode, masked):
+    """N or K not a multiple of 64 (d_model 32, 96, ...): the vector-ALU kernel, same epilogues,
+    masked rows filled bitwise as on the MFMA path."""
+    x = _rand((m, k), 110 + m, 1.0)
+    w = _rand((n, k), 111 + n, 1.0 / math.sqrt(k))
+    b = _rand((n,), 112, 0.5)
+    r = _rand((m, n), 113, 2.0)
+    v = _padded_rows(m, 114) if (masked and m >= 128) else (torch.rand(m, generator=torch.Generator().manual_seed(3)) > 0.3 if masked else None)
+    vd = None if v is None else v.to(device)
+    branch = _linear_ref(x, w, b)
+    if mode == "gelu":
+        branch = O.gelu_erf(branch)
+    if mode in ("bias", "gelu"):
+        y = ops.linear(x, w, b, mode, valid=vd)
+        ref = branch
+    else:
+        y = ops.linear(x, w, b, mode, residual=r, valid=vd)
+        ref = r.float().cpu() + branch
+    torch.cuda.synchronize()
+    got = y.cpu()
+    rows = torch.ones(m, dtype=torch.bool) if v is None else v
+    err = (got.float()[rows] - ref[rows]).abs().max().item() if rows.any() else 0.0
+    assert err <= 3e-3 * max(1.0, ref.abs().max().item()), err
+    if v is not None and (~v).any():
+        if mode == "resid_masked":
+            assert torch.equal(got[~v], r.cpu()[~v])
+        else:
+            assert _bits_zero(got[~v])
 
 
 # ---------------------------------------------------------------- QKV layout + attention
@@ -252,7 +289,7 @@ def _masks(kind, b, s, seed):
     return m
 
 
-@pytest.mark.parametrize("hd", [32, 64])
+@pytest.mark.parametrize("hd", [8, 16, 32, 64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("s", [1, 37, 64, 128, 200, 512])
 @pytest.mark.parametrize("mask_kind", ["none", "prefix", "nonprefix", "ragged_empty"])
@@ -297,8 +334,8 @@ def test_attention_benchmark_shapes(device, b, s, h, hd, causal):
 
 
 def test_attention_rejects_head_dim(device):
-    q = _rand((1, 1, 8, 16), 1)
-    vt = _rand((1, 1, 16, 64), 2)
+    q = _rand((1, 1, 8, 48), 1)
+    vt = _rand((1, 1, 48, 64), 2)
     with pytest.raises(ValueError):
         ops.attention(q, q, vt, None, False)
 

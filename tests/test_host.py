@@ -62,7 +62,9 @@ def test_workspace_bytes_monotone_and_validated():
     # C5 workspace: x, LN/ctx, Q, K, V^T, FFN hidden (fp16) ~ 144 MiB
     assert big == pytest.approx((4 * 8192 * 1024 + 2 * 1024 * 4096 + 8192 * 4096) * 2, rel=1e-3)
     with pytest.raises(ValueError):
-        _lib.workspace_bytes(1, 64, 256, 16, 1024)  # head_dim 16
+        _lib.workspace_bytes(1, 64, 240, 5, 1024)  # head_dim 48
+    with pytest.raises(ValueError):  # the megakernel's attention tasks take head_dim 32 / 64
+        _lib.workspace_bytes(1, 64, 256, 16, 1024, 2, _lib.PLAN_MEGAKERNEL)
     # megakernel: residual, context, Q/K/V^T, FFN hidden (fp16) + counters growing with layers
     m2 = _lib.workspace_bytes(1, 64, 256, 8, 1024, 2, _lib.PLAN_MEGAKERNEL)
     m64 = _lib.workspace_bytes(1, 64, 256, 8, 1024, 64, _lib.PLAN_MEGAKERNEL)
@@ -76,26 +78,32 @@ def test_workspace_bytes_monotone_and_validated():
 def test_plan_resolution():
     # measured on MI355X: few tokens with d_model <= 512 run fastest with LN fused into the QKV /
     # ffn_in tiles (C1, C2); the megakernel is slower there and is only selected explicitly
-    assert _lib.resolve_plan(1, 64, 256, _lib.PLAN_AUTO) == _lib.PLAN_FUSED_LN       # C2
-    assert _lib.resolve_plan(4, 128, 256, _lib.PLAN_AUTO) == _lib.PLAN_FUSED_LN      # C1
-    assert _lib.resolve_plan(1, 64, 256, _lib.PLAN_MEGAKERNEL) == _lib.PLAN_MEGAKERNEL
-    assert _lib.resolve_plan(1, 64, 256, _lib.PLAN_LAYERWISE) == _lib.PLAN_LAYERWISE
-    assert _lib.resolve_plan(8, 512, 512, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE     # C3
-    assert _lib.resolve_plan(2, 4096, 1024, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE   # C5
-    assert _lib.resolve_plan(1, 64, 1024, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE     # D > 512
-    assert _lib.resolve_plan(2, 4096, 512, _lib.PLAN_MEGAKERNEL) == _lib.PLAN_MEGAKERNEL
+    assert _lib.resolve_plan(1, 64, 256, 8, 1024, _lib.PLAN_AUTO) == _lib.PLAN_FUSED_LN       # C2
+    assert _lib.resolve_plan(4, 128, 256, 4, 1024, _lib.PLAN_AUTO) == _lib.PLAN_FUSED_LN      # C1
+    assert _lib.resolve_plan(1, 64, 256, 8, 1024, _lib.PLAN_MEGAKERNEL) == _lib.PLAN_MEGAKERNEL
+    assert _lib.resolve_plan(1, 64, 256, 8, 1024, _lib.PLAN_LAYERWISE) == _lib.PLAN_LAYERWISE
+    assert _lib.resolve_plan(8, 512, 512, 8, 2048, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE     # C3
+    assert _lib.resolve_plan(2, 4096, 1024, 16, 4096, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE   # C5
+    assert _lib.resolve_plan(1, 64, 1024, 16, 4096, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE     # D > 512
+    assert _lib.resolve_plan(2, 4096, 512, 8, 2048, _lib.PLAN_MEGAKERNEL) == _lib.PLAN_MEGAKERNEL
     with pytest.raises(ValueError):
-        _lib.resolve_plan(1, 64, 256, 7)
+        _lib.resolve_plan(1, 64, 256, 8, 1024, 7)
 
 
 @pytest.mark.parametrize("kwargs,ok", [
     (dict(d_model=256, num_heads=8, ffn_dim=1024), True),     # hd 32
     (dict(d_model=1024, num_heads=16, ffn_dim=4096), True),   # hd 64
     (dict(d_model=128, num_heads=4, ffn_dim=128), True),      # the reference's own D=F shape
-    (dict(d_model=256, num_heads=16, ffn_dim=1024), False),   # hd 16
-    (dict(d_model=512, num_heads=4, ffn_dim=2048), False),    # hd 128
-    (dict(d_model=96, num_heads=3, ffn_dim=128), False),      # D not a multiple of 64
-    (dict(d_model=256, num_heads=4, ffn_dim=1000), False),    # F not a multiple of 64
+    (dict(d_model=256, num_heads=16, ffn_dim=1024), True),    # hd 16
+    (dict(d_model=512, num_heads=4, ffn_dim=2048), True),     # hd 128
+    (dict(d_model=1024, num_heads=4, ffn_dim=1024), True),    # hd 256 (reference case 8)
+    (dict(d_model=32, num_heads=4, ffn_dim=32), True),        # hd 8, D = 32 (reference case 7)
+    (dict(d_model=96, num_heads=3, ffn_dim=128), True),       # hd 32, D not a multiple of 64
+    (dict(d_model=96, num_heads=2, ffn_dim=128), False),      # hd 48
+    (dict(d_model=512, num_heads=1, ffn_dim=2048), False),    # hd 512
+    (dict(d_model=256, num_heads=4, ffn_dim=1000), True),     # F a multiple of 8, not of 64
+    (dict(d_model=256, num_heads=4, ffn_dim=1004), False),    # F not a multiple of 8
+    (dict(d_model=12, num_heads=3, ffn_dim=16), False),       # hd 4, D not a multiple of 8
 ])
 def test_check_supported(kwargs, ok):
     cfg = TransformerConfig(batch_size=2, seq_len=16, num_layers=2, causal=True, **kwargs)

@@ -30,7 +30,7 @@ SIGNATURES = {
     "tt_weight_layout": (_I, [_I, _I, _I, ctypes.POINTER(_I64), ctypes.POINTER(_I64),
                               ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
     "tt_workspace_bytes": (_I, [_I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_I64)]),
-    "tt_resolve_plan": (_I, [_I, _I, _I, _I]),
+    "tt_resolve_plan": (_I, [_I, _I, _I, _I, _I, _I]),
     "tt_megakernel_status": (_I, [_P, _I, _I, _I, _I, _I, ctypes.POINTER(_I), _P]),
     "tt_megakernel_tasks": (_I, [_I, _I, _I, _I, _I, _I]),
     "tt_megakernel_trace_fwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _I, _I, _P,
@@ -101,8 +101,9 @@ def workspace_bytes(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int
     return out.value
 
 
-def resolve_plan(batch: int, seq: int, d_model: int, plan: int) -> int:
-    rc = load().tt_resolve_plan(batch, seq, d_model, plan)
+def resolve_plan(batch: int, seq: int, d_model: int, num_heads: int, ffn_dim: int,
+                 plan: int) -> int:
+    rc = load().tt_resolve_plan(batch, seq, d_model, num_heads, ffn_dim, plan)
     if rc < 0:
         check(TT_ERR_INVALID, "tt_resolve_plan")
     return rc

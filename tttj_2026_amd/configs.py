@@ -47,6 +47,25 @@ WORKLOADS: Dict[str, Workload] = {
 }
 WORKLOAD_ORDER = ("C1", "C2", "C3", "C4", "C5")
 
+# The reference's own shape table (optimized_transformer.py:22-42): case -> (batch, seq, d_model,
+# heads); every case is causal with ffn_dim = d_model and 4 layers (2 for case 14).  The HIP path
+# is not limited to these shapes; they are parity and timing cases.
+REFERENCE_CASES: Dict[int, Tuple[int, int, int, int]] = {
+    1: (64, 128, 128, 4), 2: (1, 128, 128, 4), 3: (4, 128, 128, 4), 4: (16, 128, 128, 4),
+    5: (128, 128, 128, 4), 6: (10000, 128, 128, 4), 7: (64, 128, 32, 4), 8: (64, 128, 1024, 4),
+    9: (64, 128, 128, 1), 10: (64, 128, 128, 2), 11: (64, 128, 128, 16), 12: (64, 32, 128, 4),
+    13: (64, 1024, 128, 4), 14: (32, 100000, 1024, 16),
+}
+REFERENCE_CASE_LAYERS: Dict[int, int] = {n: 2 if n == 14 else 4 for n in REFERENCE_CASES}
+
+
+def reference_case_config(case: int, batch: Optional[int] = None,
+                          seq: Optional[int] = None) -> TransformerConfig:
+    """TransformerConfig of reference case ``case`` (optionally with a smaller batch / seq)."""
+    b, s, d, h = REFERENCE_CASES[case]
+    return _cfg(b if batch is None else batch, s if seq is None else seq, d, h, d,
+                REFERENCE_CASE_LAYERS[case], True)
+
 
 def build_model(config: TransformerConfig, seed: int = SEED) -> BaselineTransformer:
     """Seeded fp32 CPU model in reference construction order (regression.py:30-44)."""

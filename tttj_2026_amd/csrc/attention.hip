@@ -1,32 +1,12 @@
-// Standalone flash-attention kernel (one block per (b, h, 128-query tile)) and the per-sequence
-// mask summary; the block itself is attention_block() in attention_block.hpp.
+// Flash-attention launches for head_dim 32, 64 and 128 (attention_kernel, one block per (b, h,
+// 128-query tile); the block itself is attention_block() in attention_block.hpp), the head_dim
+// dispatch (8 / 16: attention_small.hip, 256: attention_wide.hip) and the per-sequence mask
+// summary.  Built with the VGPR-form MFMA flag (accumulators in architectural VGPRs: 127 VGPRs at
+// head_dim 64, 190 at 128).
 #include "attention_block.hpp"
 #include "kernels.hpp"
 
 namespace tt {
-
-template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a, const int32_t* __restrict__ info) {
-  // Dynamic LDS: with statically declared tiles the compiler makes the first K-fragment read of
-  // every tile wait (vmcnt(0)) for the next tile's in-flight global -> LDS copies, serialising
-  // the prefetch; from the dynamic area it relies on the explicit waits, as intended.
-  extern __shared__ __align__(16) half att_lds[];
-  half* sk = att_lds;
-  half* sv = att_lds + 2 * kBKV * HD;
-  const int BH = a.B * a.H;
-  const int nqt = (a.S + kBQ - 1) / kBQ;
-  const int bh = blockIdx.x % BH;
-  int qt = blockIdx.x / BH;
-  if (CAUSAL) qt = nqt - 1 - qt;  // heaviest causal tiles first
-  const int b = bh / a.H;
-  int kv_end = a.S;
-  bool prefix = true;
-  if (info != nullptr) {
-    kv_end = info[b];
-    prefix = info[a.B + b] != 0;
-  }
-  attention_block<HD, CAUSAL>(a, bh, qt, kv_end, prefix, sk, sv);
-}
 
 __global__ __launch_bounds__(256) void mask_info_kernel(const uint8_t* __restrict__ mask,
                                                         int32_t* __restrict__ info, int B, int S) {
@@ -70,27 +50,32 @@ int launch_mask_info(const uint8_t* mask, int32_t* info, int batch, int seq, hip
   return launch_status("mask_info_kernel");
 }
 
+int attention_head_dim_supported(int head_dim) {
+  TT_REQUIRE(head_dim == 8 || head_dim == 16 || head_dim == 32 || head_dim == 64 ||
+                 head_dim == 128 || head_dim == 256,
+             "attention: head_dim %d not in {8, 16, 32, 64, 128, 256}", head_dim);
+  return TT_OK;
+}
+
 int launch_attention(const half* q, const half* k, const half* vt, const uint8_t* mask,
                      const int32_t* info, half* ctx, int batch, int seq, int heads, int head_dim,
                      int causal, hipStream_t stream) {
   TT_REQUIRE(batch > 0 && seq > 0 && heads > 0, "attention: bad shape");
-  TT_REQUIRE(head_dim == 32 || head_dim == 64, "attention: head_dim %d not in {32, 64}", head_dim);
+  int rc = attention_head_dim_supported(head_dim);
+  if (rc != TT_OK) return rc;
   TT_REQUIRE(mask == nullptr || info != nullptr, "attention: a mask needs its mask_info");
-  const long blocks = (long)batch * heads * ((seq + kBQ - 1) / kBQ);
-  TT_REQUIRE(blocks < (1L << 31), "attention: grid too large");
   const float scale_log2 = (1.0f / sqrtf((float)head_dim)) * 1.4426950408889634f;
-  const dim3 grid((unsigned)blocks), block(256);
   const AttnArgs args{q, k, vt, mask, ctx, batch, seq, heads, scale_log2};
-#define TT_ATT(HD, C)                                                                          \
-  hipLaunchKernelGGL((attention_kernel<HD, C>), grid, block, 4 * kBKV * HD * sizeof(half), stream, \
-                     args, info)
-  if (head_dim == 64) {
-    if (causal) TT_ATT(64, true); else TT_ATT(64, false);
-  } else {
-    if (causal) TT_ATT(32, true); else TT_ATT(32, false);
+  if (head_dim <= 16) return launch_attention_small(args, info, head_dim, causal, stream);
+  if (head_dim == 256) return launch_attention_wide(args, info, head_dim, causal, stream);
+  switch (head_dim) {
+    case 32: return causal ? launch_attention_hd<32, true>(args, info, stream)
+                           : launch_attention_hd<32, false>(args, info, stream);
+    case 64: return causal ? launch_attention_hd<64, true>(args, info, stream)
+                           : launch_attention_hd<64, false>(args, info, stream);
+    default: return causal ? launch_attention_hd<128, true>(args, info, stream)
+                           : launch_attention_hd<128, false>(args, info, stream);
   }
-#undef TT_ATT
-  return launch_status("attention_kernel");
 }
 
 }  // namespace tt

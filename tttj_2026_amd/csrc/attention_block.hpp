@@ -24,6 +24,8 @@
 
 #include "common.hpp"
 
+#include <mutex>
+
 namespace tt {
 
 constexpr int kBQ = 128;
@@ -35,10 +37,12 @@ __device__ __forceinline__ int pi23(int r) {  // swap bits 2 and 3
   return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
 }
 
-// chunk swizzle for a K tile row of HD halfs (HD/8 chunks of 16 bytes)
+// chunk swizzle for a K tile row of HD halfs (HD/8 chunks of 16 bytes): eight consecutive rows
+// read at one logical chunk land in eight different 16-byte bank groups (HD >= 64), or the four
+// chunks of a 64-byte row pair up with the row parity bits (HD = 32).
 template <int HD>
 __device__ __forceinline__ int kswz(int row, int c) {
-  if constexpr (HD == 64) return c ^ (row & 7);
+  if constexpr (HD >= 64) return c ^ (row & 7);
   else return c ^ ((row >> 1) & 3);
 }
 
@@ -72,6 +76,7 @@ struct AttnArgs {
 template <int HD, bool CAUSAL>
 __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int qt, int kv_end,
                                                 bool prefix, half* sk_base, half* sv_base) {
+  static_assert(HD == 32 || HD == 64 || HD == 128 || HD == 256, "MFMA attention head_dim");
   constexpr int KSTEPS = HD / 16;  // k-steps of the S^T MFMA
   constexpr int DB = HD / 32;      // 32-row blocks of O^T
   constexpr int KCH = HD / 8;      // 16-byte chunks per K row
@@ -297,5 +302,51 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     }
 }
 
+// Standalone launch: one block per (b, h, 128-query tile).  `info` (or nullptr without a mask)
+// holds kv_end per sequence and whether its valid keys form a prefix (mask_info_kernel).
+template <int HD, bool CAUSAL>
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a, const int32_t* __restrict__ info) {
+  // Dynamic LDS: with statically declared tiles the compiler makes the first K-fragment read of
+  // every tile wait (vmcnt(0)) for the next tile's in-flight global -> LDS copies, serialising
+  // the prefetch; from the dynamic area it relies on the explicit waits, as intended.
+  extern __shared__ __align__(16) half att_lds[];
+  half* sk = att_lds;
+  half* sv = att_lds + 2 * kBKV * HD;
+  const int BH = a.B * a.H;
+  const int nqt = (a.S + kBQ - 1) / kBQ;
+  const int bh = blockIdx.x % BH;
+  int qt = blockIdx.x / BH;
+  if (CAUSAL) qt = nqt - 1 - qt;  // heaviest causal tiles first
+  const int b = bh / a.H;
+  int kv_end = a.S;
+  bool prefix = true;
+  if (info != nullptr) {
+    kv_end = info[b];
+    prefix = info[a.B + b] != 0;
+  }
+  attention_block<HD, CAUSAL>(a, bh, qt, kv_end, prefix, sk, sv);
+}
+
+constexpr size_t attention_lds_bytes(int hd) { return 4 * (size_t)kBKV * hd * sizeof(half); }
+
+// Host side: one launch of attention_kernel<HD, CAUSAL> over every (b, h, query tile); the
+// dynamic LDS limit is raised once per instantiation (above 64 KiB for HD 256).
+template <int HD, bool CAUSAL>
+int launch_attention_hd(const AttnArgs& args, const int32_t* info, hipStream_t stream) {
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [] {
+    attr = hipFuncSetAttribute((const void*)attention_kernel<HD, CAUSAL>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)attention_lds_bytes(HD));
+  });
+  if (attr != hipSuccess)
+    return fail(TT_ERR_HIP, "hipFuncSetAttribute(attention hd %d): %s", HD, hipGetErrorString(attr));
+  const long blocks = (long)args.B * args.H * ((args.S + kBQ - 1) / kBQ);
+  TT_REQUIRE(blocks < (1L << 31), "attention: grid too large");
+  hipLaunchKernelGGL((attention_kernel<HD, CAUSAL>), dim3((unsigned)blocks), dim3(256),
+                     attention_lds_bytes(HD), stream, args, info);
+  return launch_status("attention_kernel");
+}
 
 }  // namespace tt

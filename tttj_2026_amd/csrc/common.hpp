@@ -64,6 +64,16 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
+// Workgroup barrier without the memory fence that __syncthreads() implies (that fence waits for
+// every in-flight global load, vmcnt(0), which would drain a multi-stage copy pipeline).  Callers
+// wait for exactly the copies they need with wait_vmcnt first.  The empty asm statements keep the
+// compiler from moving memory operations across the barrier.
+__device__ __forceinline__ void raw_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane l writes LDS bytes
 // [16 l, 16 l + 16) after the wave-uniform destination `lds_dst`.
 __device__ __forceinline__ void lds_copy16(const half* src, half* lds_dst) {

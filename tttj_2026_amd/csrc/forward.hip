@@ -80,8 +80,9 @@ static int check_model_shape(int B, int S, int D, int H, int F, int L) {
   TT_REQUIRE(B > 0 && S > 0 && D > 0 && H > 0 && F > 0 && L > 0,
              "transformer: non-positive shape B=%d S=%d D=%d H=%d F=%d L=%d", B, S, D, H, F, L);
   TT_REQUIRE(D % H == 0, "transformer: d_model %d not divisible by heads %d", D, H);
-  TT_REQUIRE(D / H == 32 || D / H == 64, "transformer: head_dim %d not in {32, 64}", D / H);
-  TT_REQUIRE(D % 64 == 0 && F % 64 == 0, "transformer: d_model %d and ffn_dim %d must be multiples of 64", D, F);
+  const int rc = attention_head_dim_supported(D / H);
+  if (rc != TT_OK) return rc;
+  TT_REQUIRE(D % 8 == 0 && F % 8 == 0, "transformer: d_model %d and ffn_dim %d must be multiples of 8", D, F);
   TT_REQUIRE(D <= 8192, "transformer: d_model %d > 8192", D);
   TT_REQUIRE((int64_t)B * S < (1LL << 31) / 8, "transformer: too many tokens");
   return TT_OK;
@@ -124,11 +125,16 @@ static constexpr int kMegaMaxDModel = 512;  // the megakernel keeps a LayerNorm'
 // GEMM tiles).
 static constexpr int64_t kFusedLnMaxTokens = 1024;
 
-static int resolve_plan(int plan, int B, int S, int D) {
+// The automatic plan only picks a fused plan for shapes its kernels take (64-multiple d_model
+// and ffn_dim; head_dim 32 / 64 for the megakernel); an explicit plan is returned as asked and
+// the forward reports an unsupported shape as an error.
+static int resolve_plan(int plan, int B, int S, int D, int H, int F) {
   if (plan != TT_PLAN_AUTO) return plan;
   const int64_t T = (int64_t)B * S;
-  if (T <= kMegaMaxTokens && D <= kMegaMaxDModel) return TT_PLAN_MEGAKERNEL;
-  if (T <= kFusedLnMaxTokens && D <= kMegaMaxDModel) return TT_PLAN_FUSED_LN;
+  const bool tiles64 = D % 64 == 0 && F % 64 == 0 && D <= kMegaMaxDModel;
+  const int hd = H > 0 ? D / H : 0;
+  if (T <= kMegaMaxTokens && tiles64 && (hd == 32 || hd == 64)) return TT_PLAN_MEGAKERNEL;
+  if (T <= kFusedLnMaxTokens && tiles64) return TT_PLAN_FUSED_LN;
   return TT_PLAN_LAYERWISE;
 }
 
@@ -138,7 +144,7 @@ extern "C" int tt_workspace_bytes(int batch, int seq, int d_model, int num_heads
   if (rc != TT_OK) return rc;
   TT_REQUIRE(bytes != nullptr, "workspace_bytes: null output");
   TT_REQUIRE(plan >= TT_PLAN_AUTO && plan <= TT_PLAN_FUSED_LN, "workspace_bytes: bad plan %d", plan);
-  plan = resolve_plan(plan, batch, seq, d_model);
+  plan = resolve_plan(plan, batch, seq, d_model, num_heads, ffn_dim);
   if (plan == TT_PLAN_MEGAKERNEL) {
     if ((rc = megakernel_supported(batch, seq, d_model, num_heads, ffn_dim, num_layers)) != TT_OK)
       return rc;
@@ -149,13 +155,16 @@ extern "C" int tt_workspace_bytes(int batch, int seq, int d_model, int num_heads
   return TT_OK;
 }
 
-extern "C" int tt_resolve_plan(int batch, int seq, int d_model, int plan) {
-  if (plan < TT_PLAN_AUTO || plan > TT_PLAN_FUSED_LN || batch <= 0 || seq <= 0 || d_model <= 0) {
-    fail(TT_ERR_INVALID, "resolve_plan: bad arguments (batch=%d seq=%d d_model=%d plan=%d)",
-         batch, seq, d_model, plan);
+extern "C" int tt_resolve_plan(int batch, int seq, int d_model, int num_heads, int ffn_dim,
+                               int plan) {
+  if (plan < TT_PLAN_AUTO || plan > TT_PLAN_FUSED_LN || batch <= 0 || seq <= 0 || d_model <= 0 ||
+      num_heads <= 0 || ffn_dim <= 0) {
+    fail(TT_ERR_INVALID,
+         "resolve_plan: bad arguments (batch=%d seq=%d d_model=%d heads=%d ffn=%d plan=%d)", batch,
+         seq, d_model, num_heads, ffn_dim, plan);
     return -1;
   }
-  return resolve_plan(plan, batch, seq, d_model);
+  return resolve_plan(plan, batch, seq, d_model, num_heads, ffn_dim);
 }
 
 extern "C" int tt_megakernel_trace_fwd(const void* weights, const void* x, const uint8_t* mask,
@@ -201,7 +210,7 @@ extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint
   TT_REQUIRE(plan >= TT_PLAN_AUTO && plan <= TT_PLAN_FUSED_LN, "transformer: bad plan %d", plan);
   const int B = batch, S = seq, D = d_model, H = num_heads, F = ffn_dim, L = num_layers;
   const int T = B * S, hd = D / H;
-  if (resolve_plan(plan, B, S, D) == TT_PLAN_MEGAKERNEL) {
+  if (resolve_plan(plan, B, S, D, H, F) == TT_PLAN_MEGAKERNEL) {
     const Layout lay = weight_layout(D, F, L);
     return launch_megakernel((const half*)weights, lay.off, lay.stride, lay.final_off,
                              (const half*)x, mask, (half*)y, (char*)workspace, workspace_bytes, B,
@@ -224,8 +233,9 @@ extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint
   }
   // TT_PLAN_FUSED_LN: LN1 / LN2 are computed inside the QKV / ffn_in tiles (launch_ln_tile), five
   // launches per layer instead of seven.
-  const bool fused_ln = resolve_plan(plan, B, S, D) == TT_PLAN_FUSED_LN;
-  if (fused_ln && (rc = ln_tile_supported(D, F)) != TT_OK) return rc;
+  const bool fused_ln = resolve_plan(plan, B, S, D, H, F) == TT_PLAN_FUSED_LN;
+  if (fused_ln && ((rc = ln_tile_supported(D, 3 * D)) != TT_OK || (rc = ln_tile_supported(D, F)) != TT_OK))
+    return rc;
   const half* cur = (const half*)x;
   for (int l = 0; l < L; ++l) {
     const half* w = wts + (size_t)l * lay.stride;

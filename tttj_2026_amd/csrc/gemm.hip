@@ -170,16 +170,20 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
 
   // Copy sources: copy i of this wave fills 8-row group wave + 4 i of the stage.  X rows past M
   // are clamped to M - 1 (valid memory whose results are never stored).
+  // Offsets are relative to the block's first X row and W row (64-bit bases), so M * K may
+  // exceed 2^31 (long sequences); BM * K and BN * K stay far below it.
   const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
+  const half* Xb = X + (size_t)m0 * K;
+  const half* Wb = W + (size_t)n0 * K;
   int src_off[NL];
 #pragma unroll
   for (int i = 0; i < NL; ++i) {
     const int r = (wave + 4 * i) * 8 + lrow;
-    if (i < XL) src_off[i] = min(m0 + r, M - 1) * K + lchunk * 8;
-    else src_off[i] = (n0 + r - BM) * K + lchunk * 8;
+    if (i < XL) src_off[i] = min(r, M - 1 - m0) * K + lchunk * 8;
+    else src_off[i] = (r - BM) * K + lchunk * 8;
   }
   auto copy = [&](int i, int k0, half* stage) {
-    const half* base = (i < XL) ? X : W;
+    const half* base = (i < XL) ? Xb : Wb;
     lds_copy16(base + src_off[i] + k0, stage + (wave + 4 * i) * 8 * kBK);
   };
 
@@ -393,6 +397,97 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
   }
 }
 
+// Small-shape GEMM for projections whose N or K is not a multiple of 64 (d_model 32 and the
+// like): one thread computes 4 consecutive outputs of one row with fp32 FMAs, 16-byte loads of
+// X and W rows (K % 8 == 0), and the same epilogue semantics as gemm_kernel, element by element.
+// These shapes are a few MFLOP; the MFMA tiles are kept for everything else.
+template <int MODE>
+__global__ __launch_bounds__(256) void gemm_small_kernel(const half* __restrict__ X,
+                                                         const half* __restrict__ W, int M, int N,
+                                                         int K, EpiArgs ep) {
+  const int ngroups = N / 4;
+  const long g = (long)blockIdx.x * 256 + threadIdx.x;
+  if (g >= (long)M * ngroups) return;
+  const int m = (int)(g / ngroups), n = (int)(g - (long)m * ngroups) * 4;
+  const half* xr = X + (size_t)m * K;
+  const half* wr = W + (size_t)n * K;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < K; k += 8) {
+    const half8 xv = *(const half8*)(xr + k);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const half8 wv = *(const half8*)(wr + (size_t)e * K + k);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[e] = fmaf((float)xv[t], (float)wv[t], acc[e]);
+    }
+  }
+  const bool keep = ep.valid == nullptr || ep.valid[m] != 0;
+  half4 hv;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float v = acc[e] + (float)ep.bias[n + e];
+    if constexpr (MODE == TT_EPI_BIAS_GELU) v = gelu_erf(v);
+    hv[e] = (half)v;
+  }
+  if constexpr (MODE == TT_EPI_QKV) {
+    const int D = ep.d_model, hd = ep.head_dim, S = ep.seq;
+    const size_t plane = (size_t)ep.batch * S * D;
+    const int bb = m / S, sq = m - bb * S;
+    if (!keep) hv = half4{(half)0.f, (half)0.f, (half)0.f, (half)0.f};
+    const int which = n / D, nn = n - which * D;
+    const int hh = nn / hd, d = nn - hh * hd;  // hd % 4 == 0: the 4 outputs share a head
+    if (which < 2) {
+      *(half4*)(ep.y + which * plane + (((size_t)bb * ep.heads + hh) * S + sq) * hd + d) = hv;
+    } else {
+      const size_t ldv = (size_t)(S + 63) / 64 * 64;
+      half* vt = ep.y + 2 * plane + (((size_t)bb * ep.heads + hh) * hd + d) * ldv + sq;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vt[(size_t)e * ldv] = hv[e];
+    }
+  } else {
+    half* dst = ep.y + (size_t)m * ep.ldy + n;
+    if constexpr (MODE == TT_EPI_RESID_MASKED || MODE == TT_EPI_MASKED_RESID) {
+      const half4 rv = *(const half4*)(ep.resid + (size_t)m * ep.ldy + n);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (MODE == TT_EPI_RESID_MASKED)
+          hv[e] = keep ? (half)((float)rv[e] + (float)hv[e]) : rv[e];
+        else
+          hv[e] = keep ? (half)((float)rv[e] + (float)hv[e]) : (half)0.f;
+      }
+    } else if (!keep) {
+      hv = half4{(half)0.f, (half)0.f, (half)0.f, (half)0.f};
+    }
+    *(half4*)dst = hv;
+  }
+}
+
+static int run_small(int mode, const half* x, const half* w, int m, int n, int k,
+                     const EpiArgs& ep, hipStream_t stream) {
+  const long threads = (long)m * (n / 4);
+  const long blocks = (threads + 255) / 256;
+  TT_REQUIRE(blocks < (1L << 31), "linear: grid too large");
+  const dim3 grid((unsigned)blocks), block(256);
+  switch (mode) {
+    case TT_EPI_BIAS:
+      hipLaunchKernelGGL(gemm_small_kernel<TT_EPI_BIAS>, grid, block, 0, stream, x, w, m, n, k, ep);
+      break;
+    case TT_EPI_BIAS_GELU:
+      hipLaunchKernelGGL(gemm_small_kernel<TT_EPI_BIAS_GELU>, grid, block, 0, stream, x, w, m, n, k, ep);
+      break;
+    case TT_EPI_RESID_MASKED:
+      hipLaunchKernelGGL(gemm_small_kernel<TT_EPI_RESID_MASKED>, grid, block, 0, stream, x, w, m, n, k, ep);
+      break;
+    case TT_EPI_MASKED_RESID:
+      hipLaunchKernelGGL(gemm_small_kernel<TT_EPI_MASKED_RESID>, grid, block, 0, stream, x, w, m, n, k, ep);
+      break;
+    default:
+      hipLaunchKernelGGL(gemm_small_kernel<TT_EPI_QKV>, grid, block, 0, stream, x, w, m, n, k, ep);
+      break;
+  }
+  return launch_status("gemm_small_kernel");
+}
+
 // ---- host-side tile selection ----
 struct TileCfg {
   int bm, bn;
@@ -464,10 +559,13 @@ static int device_cus() {
 int launch_linear(const half* x, const half* w, int m, int n, int k, const EpiArgs& ep,
                   hipStream_t stream) {
   TT_REQUIRE(m >= 0 && n > 0 && k > 0, "linear: bad shape m=%d n=%d k=%d", m, n, k);
-  TT_REQUIRE(k % kBK == 0, "linear: K=%d must be a multiple of %d", k, kBK);
-  TT_REQUIRE(n % 64 == 0, "linear: N=%d must be a multiple of 64", n);
-  TT_REQUIRE((int64_t)m * k < (1LL << 31) && (int64_t)n * k < (1LL << 31),
-             "linear: operands of more than 2^31 elements (m=%d n=%d k=%d)", m, n, k);
+  TT_REQUIRE(k % 8 == 0 && n % 8 == 0, "linear: N=%d and K=%d must be multiples of 8", n, k);
+  TT_REQUIRE((int64_t)n * k < (1LL << 31), "linear: weight of more than 2^31 elements (n=%d k=%d)",
+             n, k);
+  if (ep.mode == TT_EPI_RESID_MASKED || ep.mode == TT_EPI_MASKED_RESID || ep.mode == TT_EPI_BIAS ||
+      ep.mode == TT_EPI_BIAS_GELU)
+    TT_REQUIRE(ep.ldy >= n && ep.ldy % 8 == 0, "linear: ldy=%d must be >= N=%d and a multiple of 8",
+               ep.ldy, n);
   TT_REQUIRE(ep.mode >= TT_EPI_BIAS && ep.mode <= TT_EPI_QKV, "linear: bad epilogue %d", ep.mode);
   TT_REQUIRE(ep.bias != nullptr && ep.y != nullptr, "linear: null bias/output");
   if (ep.mode == TT_EPI_RESID_MASKED || ep.mode == TT_EPI_MASKED_RESID)
@@ -480,6 +578,7 @@ int launch_linear(const half* x, const half* w, int m, int n, int k, const EpiAr
                ep.batch, ep.seq, ep.heads, ep.head_dim);
   }
   if (m == 0) return TT_OK;
+  if (k % kBK != 0 || n % 64 != 0) return run_small(ep.mode, x, w, m, n, k, ep, stream);
   const int tile = pick_tile(m, n, k, device_cus());
   switch (ep.mode) {
     case TT_EPI_BIAS: return run_mode<TT_EPI_BIAS>(tile, x, w, m, n, k, ep, stream);

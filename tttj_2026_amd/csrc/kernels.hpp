@@ -26,6 +26,15 @@ int launch_mask_info(const uint8_t* mask, int32_t* info, int batch, int seq, hip
 int launch_attention(const half* q, const half* k, const half* vt, const uint8_t* mask,
                      const int32_t* info, half* ctx, int batch, int seq, int heads, int head_dim,
                      int causal, hipStream_t stream);
+int attention_head_dim_supported(int head_dim);
+
+struct AttnArgs;
+// head_dim 256: the MFMA flash block with accumulators in AGPRs (attention_wide.hip).
+int launch_attention_wide(const AttnArgs& args, const int32_t* info, int head_dim, int causal,
+                          hipStream_t stream);
+// head_dim 8 / 16: one lane per query, scores and P V on the vector ALUs (attention_small.hip).
+int launch_attention_small(const AttnArgs& args, const int32_t* info, int head_dim, int causal,
+                           hipStream_t stream);
 
 // Persistent whole-model megakernel (megakernel.hip).  The workspace must be zero-filled before
 // its first use and then reused unchanged between launches of the same shape.

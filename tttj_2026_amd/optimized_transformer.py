@@ -3,9 +3,10 @@
 Drop-in for ``optimized_transformer.make_optimized_transformer`` (optimized_transformer.py:69-93):
 the same signature and the same ``forward(x, valid_token_mask=None)`` contract
 (kernels/sequence_resident.py:227-233).  Instead of the reference's table of 14 fixed shapes
-(optimized_transformer.py:22-66) any configuration with ``head_dim in {32, 64}`` and ``d_model``,
-``ffn_dim`` multiples of 64 is accepted, causal or not; anything else raises ``ValueError`` before
-any work, as the reference does for unsupported shapes.
+(optimized_transformer.py:22-66) any configuration with ``head_dim in {8, 16, 32, 64, 128, 256}``,
+``d_model`` and ``ffn_dim`` multiples of 8 and ``d_model <= 8192`` is accepted, causal or not --
+every shape of that table included (``SUPPORTED_HEAD_DIMS``); anything else raises
+``ValueError`` before any work, as the reference does for unsupported shapes.
 
 The module packs the parameter model's fp16 weights once (``prepare``) into the layout of
 ``tt_weight_layout`` and runs every forward as one call into the HIP library on the caller's
@@ -33,6 +34,9 @@ PLAN_AUTO, PLAN_LAYERWISE, PLAN_MEGAKERNEL, PLAN_FUSED_LN = (
     _lib.PLAN_AUTO, _lib.PLAN_LAYERWISE, _lib.PLAN_MEGAKERNEL, _lib.PLAN_FUSED_LN)
 
 
+SUPPORTED_HEAD_DIMS = (8, 16, 32, 64, 128, 256)
+
+
 def check_supported(config) -> None:
     """Raise ValueError unless the HIP path implements ``config`` (a TransformerConfig-like)."""
     d, h, f = config.d_model, config.num_heads, config.ffn_dim
@@ -42,10 +46,10 @@ def check_supported(config) -> None:
     elif d % h != 0:
         problems.append(f"d_model {d} not divisible by num_heads {h}")
     else:
-        if d // h not in (32, 64):
-            problems.append(f"head_dim {d // h} not in (32, 64)")
-        if d % 64 or f % 64:
-            problems.append("d_model and ffn_dim must be multiples of 64")
+        if d // h not in SUPPORTED_HEAD_DIMS:
+            problems.append(f"head_dim {d // h} not in {SUPPORTED_HEAD_DIMS}")
+        if d % 8 or f % 8:
+            problems.append("d_model and ffn_dim must be multiples of 8")
         if d > 8192:
             problems.append("d_model must be <= 8192")
     if problems:
@@ -198,7 +202,7 @@ class OptimizedTransformer(nn.Module):
         y = torch.empty_like(x)
         if batch * seq == 0:
             return y
-        plan = _lib.resolve_plan(batch, seq, cfg.d_model, self.plan)
+        plan = _lib.resolve_plan(batch, seq, cfg.d_model, cfg.num_heads, cfg.ffn_dim, self.plan)
         ws = self._workspace(batch, seq, plan, x.device)
         stream = torch.cuda.current_stream(x.device).cuda_stream
         rc = self._lib.tt_transformer_fwd(
