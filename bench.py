@@ -14,6 +14,11 @@ tokens/s = B*S / p50.  The K timed steps are also bracketed by a device synchron
 sides, which gives ``ms_per_step``.  Inside the same run each kernel of one layer is timed in
 isolation (HIP events on the stream it is launched on) to give the roofline of the dominant
 kernel, and the CPU fp32 oracle is timed on a bounded sample on the host cores.
+
+    python bench.py --mode cases
+
+times the reference's own 14-case shape table (optimized_transformer.py:22-42) against eager fp16
+instead and prints that as its one JSON line.
 """
 
 from __future__ import annotations
@@ -30,7 +35,8 @@ import time
 import torch
 
 from tttj_2026_amd import make_optimized_transformer, ops, roofline
-from tttj_2026_amd.configs import WORKLOADS, WORKLOAD_ORDER, build_model, workload_inputs
+from tttj_2026_amd.configs import (REFERENCE_CASES, SEED, WORKLOADS, WORKLOAD_ORDER, build_model,
+                                   make_inputs, reference_case_config, workload_inputs)
 
 METRIC = "p50 fwd latency (us) per config; fp16 MFMA TFLOP/s as % of MI355X peak"
 PEAK_TFLOPS = roofline.MI355X_FP16_DENSE_TFLOPS
@@ -66,12 +72,16 @@ def lengths_of(mask, cfg):
 
 
 def bench_workload(name, steps, warmup, rounds, eager, dev):
-    w = WORKLOADS[name]
-    cfg = w.config
+    x16, mask = workload_inputs(name)
+    return bench_model(WORKLOADS[name].config, x16, mask, steps, warmup, rounds, eager, dev)
+
+
+def bench_model(cfg, x16, mask, steps, warmup, rounds, eager, dev, xd=None):
+    """Alternating rounds of optimized and eager fp16 forwards, per-call HIP-event times."""
     model = build_model(cfg).half().to(dev).eval()
     opt = make_optimized_transformer(copy.deepcopy(model))
-    x16, mask = workload_inputs(name)
-    xd = x16.to(dev)
+    if xd is None:
+        xd = x16.to(dev)
     md = None if mask is None else mask.to(dev)
     with torch.inference_mode():
         for _ in range(warmup):
@@ -240,6 +250,37 @@ def cpu_baseline(name, budget_s, gpu_out=None):
     return result
 
 
+def bench_reference_cases(dev, rounds, eager):
+    """The reference's own 14-case table (optimized_transformer.py:22-42; causal, F = D, no mask):
+    optimized vs eager fp16 p50 per case.  Case 14 (S = 100000) has no eager number: its score
+    tensor alone would be B*H*S^2 fp16 elements (10 PB)."""
+    out = {}
+    for case in sorted(REFERENCE_CASES):
+        cfg = reference_case_config(case)
+        heavy = cfg.batch_size * cfg.seq_len >= 1_000_000
+        if case == 14:   # inputs made on the GPU (3.2M x 1024): host generation would take minutes
+            g = torch.Generator(device=dev).manual_seed(SEED + 100 + case)
+            xd = torch.randn(cfg.batch_size, cfg.seq_len, cfg.d_model, generator=g,
+                             device=dev).half()
+            x16 = None
+        else:
+            x16, _ = make_inputs(cfg, False, SEED + 100 + case)
+            xd = None
+        res, _ = bench_model(cfg, x16, None, 3 if case == 14 else (10 if heavy else 50),
+                             1 if case == 14 else (3 if heavy else 20), 1 if heavy else rounds,
+                             eager and case != 14, dev, xd=xd)
+        res["shape_b_s_d_h"] = list(REFERENCE_CASES[case])
+        res["layers"] = cfg.num_layers
+        out[str(case)] = res
+        print(f"[cases] {case} {REFERENCE_CASES[case]} p50 {res['p50_us']:.1f} us"
+              + (f" eager {res['eager_p50_us']:.1f} us" if "eager_p50_us" in res else ""),
+              file=sys.stderr, flush=True)
+    sp = [v["speedup_vs_eager"] for v in out.values() if "speedup_vs_eager" in v]
+    return {"mode": "reference_cases", "cases": out, "n_with_eager": len(sp),
+            "geomean_speedup_vs_eager": math.exp(sum(map(math.log, sp)) / len(sp)) if sp else None,
+            "gpu": torch.cuda.get_device_name(dev)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -251,9 +292,10 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU oracle work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-eager", action="store_true")
-    ap.add_argument("--mode", default="full", choices=("full", "kernels"),
+    ap.add_argument("--mode", default="full", choices=("full", "kernels", "cases"),
                     help="kernels: only run each kernel of one layer (and a copy of known size) "
-                         "a few times, for rocprofv3 counter runs")
+                         "a few times, for rocprofv3 counter runs; cases: time the reference's "
+                         "own 14-case shape table against eager fp16 (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -266,6 +308,9 @@ def main() -> int:
     dev = torch.device("cuda:0")
     name = args.workload
     cfg = WORKLOADS[name].config
+    if args.mode == "cases":
+        print(json.dumps(bench_reference_cases(dev, args.rounds, not args.no_eager)))
+        return 0
     if args.mode == "kernels":
         copy_calibration(dev)
         res = kernel_breakdown(name, dev, iters=args.steps)
