@@ -335,7 +335,9 @@ __device__ void mk_gemm_tile(const half* A, const half* W, int K, int row0, int 
     else if (kt < pro) newer = 2 * (pro - 1 - kt) + 4 * (issued - pro);
     else newer = 4 * (issued - 1 - kt);
     wait_newer(newer);
-    __syncthreads();  // step kt visible to all waves; step kt - 1's buffer is free
+    // Step kt visible to all waves; step kt - 1's buffer is free.  A barrier without the memory
+    // fence of __syncthreads(), whose vmcnt(0) would also wait for the later steps' copies.
+    raw_barrier();
     const int nxt = kt + R::NS - 1;
     if (nxt < nk) {
       mk_copy_w(W, K, n0, nxt * 64, R::w(lds, nxt));
