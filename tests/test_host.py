@@ -86,6 +86,11 @@ def test_plan_resolution():
     assert _lib.resolve_plan(2, 4096, 1024, 16, 4096, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE   # C5
     assert _lib.resolve_plan(1, 64, 1024, 16, 4096, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE     # D > 512
     assert _lib.resolve_plan(2, 4096, 512, 8, 2048, _lib.PLAN_MEGAKERNEL) == _lib.PLAN_MEGAKERNEL
+    # the reference's D = 128 cases: fused LN up to 2048 tokens (case 4), layer-wise beyond (case 1)
+    assert _lib.resolve_plan(16, 128, 128, 4, 128, _lib.PLAN_AUTO) == _lib.PLAN_FUSED_LN
+    assert _lib.resolve_plan(64, 128, 128, 4, 128, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE
+    # shapes the fused tiles do not take fall back to layer-wise (d_model 32: N = 96)
+    assert _lib.resolve_plan(4, 128, 32, 4, 32, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE
     with pytest.raises(ValueError):
         _lib.resolve_plan(1, 64, 256, 8, 1024, 7)
 
