@@ -80,6 +80,25 @@ def test_input_scales(device, scale):
     assert res["passed"], res
 
 
+@pytest.mark.parametrize("plan", ["auto", "layerwise"])
+@pytest.mark.parametrize("b,s,d,h,f,causal,masked", [
+    (1, 64, 256, 8, 1024, True, False),      # C2 shape: ffn_out K = 1024 over 4 tiles
+    (2, 96, 256, 4, 2048, True, True),       # padded rows, K = 2048
+    (4, 128, 512, 8, 2048, False, True),
+    (3, 40, 128, 2, 512, False, False),      # partial row tile, K = 512
+])
+def test_few_tokens_long_k(device, plan, b, s, d, h, f, causal, masked):
+    """Few tokens and long K (small grids, partial row tiles, padded rows), both plans."""
+    from tttj_2026_amd import PLAN_AUTO
+    cfg = TransformerConfig(b, s, d, h, f, 2, causal)
+    model = build_model(cfg, seed=11)
+    x16, mask = make_inputs(cfg, masked, 12)
+    res, _, _, _ = _run(model, x16, mask, device,
+                        plan=PLAN_AUTO if plan == "auto" else PLAN_LAYERWISE)
+    assert res["passed"], res
+    assert res["repeat_identical"]
+
+
 def test_runtime_shape_differs_from_config(device):
     """Any (B, S) works at run time; only d_model/heads/ffn/layers come from the config."""
     cfg = TransformerConfig(4, 128, 256, 4, 1024, 2, False)
