@@ -137,3 +137,21 @@ def test_c_abi_rejects_bad_arguments_without_launching():
                                 None) == _lib.TT_ERR_INVALID
     assert "head_dim" in _lib.last_error()
     assert lib.tt_gemm_tile_override(99) == _lib.TT_ERR_INVALID
+
+
+def test_reference_case_table_is_supported():
+    """Every shape of the reference's case table (optimized_transformer.py:22-42) passes the
+    constructor's check, and the C ABI sizes its workspace (case 14: 3.2M tokens, > 2^31 GEMM
+    operand elements) without refusing it."""
+    from tttj_2026_amd.configs import REFERENCE_CASES, REFERENCE_CASE_LAYERS, reference_case_config
+    assert len(REFERENCE_CASES) == 14 and REFERENCE_CASE_LAYERS[14] == 2 and REFERENCE_CASE_LAYERS[1] == 4
+    for case in REFERENCE_CASES:
+        cfg = reference_case_config(case)
+        assert cfg.causal and cfg.ffn_dim == cfg.d_model
+        check_supported(cfg)
+        n = _lib.workspace_bytes(cfg.batch_size, cfg.seq_len, cfg.d_model, cfg.num_heads,
+                                 cfg.ffn_dim, cfg.num_layers)
+        t = cfg.batch_size * cfg.seq_len
+        assert n >= (5 * t * cfg.d_model + t * cfg.ffn_dim) * 2
+    cfg = reference_case_config(14)
+    assert cfg.batch_size * cfg.seq_len * cfg.d_model > 2 ** 31
