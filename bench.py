@@ -65,6 +65,19 @@ def time_calls(fn, iters):
     return [s.elapsed_time(e) for s, e in zip(starts, ends)]
 
 
+def loop_time(fn, iters):
+    """Average ms per call of ``fn`` over ``iters`` back-to-back calls (HIP events)."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(iters):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters
+
+
 def lengths_of(mask, cfg):
     if mask is None:
         return None
@@ -157,8 +170,10 @@ def kernel_breakdown(name, dev, iters=20):
     for kname, (fn, per_layer, bound, work) in kernels.items():
         for _ in range(3):
             fn()
-        t = statistics.median(time_calls(fn, iters))
-        # ops wrappers allocate outputs; the allocator is warm, so events see the kernel itself
+        # average over back-to-back launches between one pair of HIP events on the launch stream
+        # (per-call event pairs would also count the host's launch latency as GPU time); the
+        # median of 3 such loops
+        t = statistics.median(loop_time(fn, iters) for _ in range(3))
         entry = {"avg_ms": t, "per_layer": per_layer, "bound": bound,
                  "ms_per_forward": t * per_layer * cfg.num_layers}
         if bound == "mfma":
