@@ -155,3 +155,23 @@ def test_reference_case_table_is_supported():
         assert n >= (5 * t * cfg.d_model + t * cfg.ffn_dim) * 2
     cfg = reference_case_config(14)
     assert cfg.batch_size * cfg.seq_len * cfg.d_model > 2 ** 31
+
+
+def test_case_number_for_model_mirrors_reference():
+    """case_number_for_model: the reference's table lookup (optimized_transformer.py:45-66) with its
+    error message for shapes outside the table."""
+    from tttj_2026_amd import IMPLEMENTED_CASES, case_number_for_model
+    from tttj_2026_amd.configs import reference_case_config
+
+    class Holder:  # only .config is read
+        def __init__(self, config):
+            self.config = config
+
+    for case in IMPLEMENTED_CASES:
+        assert case_number_for_model(Holder(reference_case_config(case))) == case
+    with pytest.raises(ValueError, match="no optimized transformer is implemented for shape="):
+        case_number_for_model(Holder(WORKLOADS["C5"].config))  # ffn_dim = 4 d_model
+    with pytest.raises(ValueError, match="layers=3"):
+        cfg = reference_case_config(1)
+        case_number_for_model(Holder(TransformerConfig(cfg.batch_size, cfg.seq_len, cfg.d_model,
+                                                       cfg.num_heads, cfg.ffn_dim, 3, True)))

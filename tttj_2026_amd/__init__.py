@@ -11,8 +11,11 @@ from .optimized_transformer import (
     PLAN_FUSED_LN,
     PLAN_LAYERWISE,
     PLAN_MEGAKERNEL,
+    IMPLEMENTED_CASE_LAYERS,
+    IMPLEMENTED_CASES,
     GraphedOptimizedTransformer,
     OptimizedTransformer,
+    case_number_for_model,
     check_supported,
     make_optimized_transformer,
     pack_model_weights,
@@ -26,6 +29,9 @@ __all__ = [
     "make_optimized_transformer",
     "pack_model_weights",
     "check_supported",
+    "case_number_for_model",
+    "IMPLEMENTED_CASES",
+    "IMPLEMENTED_CASE_LAYERS",
     "PLAN_AUTO",
     "PLAN_LAYERWISE",
     "PLAN_MEGAKERNEL",

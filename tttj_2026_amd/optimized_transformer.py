@@ -29,12 +29,32 @@ import torch
 import torch.nn as nn
 
 from . import _lib
+from .configs import REFERENCE_CASE_LAYERS, REFERENCE_CASES
 
 PLAN_AUTO, PLAN_LAYERWISE, PLAN_MEGAKERNEL, PLAN_FUSED_LN = (
     _lib.PLAN_AUTO, _lib.PLAN_LAYERWISE, _lib.PLAN_MEGAKERNEL, _lib.PLAN_FUSED_LN)
 
 
 SUPPORTED_HEAD_DIMS = (8, 16, 32, 64, 128, 256)
+
+# The reference's public case table under its own names (optimized_transformer.py:22-42); this
+# build accepts those shapes and more (check_supported), the table is kept for callers that use it.
+IMPLEMENTED_CASES = REFERENCE_CASES
+IMPLEMENTED_CASE_LAYERS = REFERENCE_CASE_LAYERS
+
+
+def case_number_for_model(parameter_model: nn.Module) -> int:
+    """The reference case (optimized_transformer.py:45-66) whose shape ``parameter_model`` has:
+    causal, ffn_dim == d_model, (batch, seq, d_model, heads) and the layer count of one table
+    entry; ``ValueError`` otherwise, with the reference's message."""
+    cfg = parameter_model.config
+    shape = (cfg.batch_size, cfg.seq_len, cfg.d_model, cfg.num_heads)
+    if cfg.ffn_dim == cfg.d_model and cfg.causal:
+        for case, case_shape in IMPLEMENTED_CASES.items():
+            if shape == case_shape and cfg.num_layers == IMPLEMENTED_CASE_LAYERS[case]:
+                return case
+    raise ValueError(f"no optimized transformer is implemented for shape={shape}, "
+                     f"ffn_dim={cfg.ffn_dim}, layers={cfg.num_layers}, causal={cfg.causal}")
 
 
 def check_supported(config) -> None:
