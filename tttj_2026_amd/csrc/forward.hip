@@ -120,13 +120,13 @@ extern "C" int tt_weight_layout(int d_model, int ffn_dim, int num_layers,
 // everywhere until that changes; the megakernel is selected explicitly with TT_PLAN_MEGAKERNEL.
 static constexpr int64_t kMegaMaxTokens = 0;
 static constexpr int kMegaMaxDModel = 512;  // the megakernel keeps a LayerNorm'd 64 x D tile in LDS
-// Token count up to which the automatic plan computes LN1 / LN2 inside the QKV / ffn_in tiles
-// (fewer launches on the latency-bound path; beyond it the 64 x 64 tiles lose to the layer-wise
-// GEMM tiles).  Measured on MI355X: C1 / C2 (d_model 256, 512 / 64 tokens) 77 / 138 us fused
-// against 80 / 141 layer-wise; d_model 128 still gains at 2048 tokens (101 against 114 us, the
-// reference's case 4) and loses from 8192 (161 against 147 us, its case 1).
-static constexpr int64_t kFusedLnMaxTokens = 1024;
-static constexpr int64_t kFusedLnMaxTokensNarrow = 2048;  // d_model <= 128
+// The automatic plan computes LN1 / LN2 inside the QKV / ffn_in 64 x 64 tiles (fewer launches on
+// the latency-bound path) only for narrow models with few tokens: measured on MI355X, d_model 128
+// gains up to 2048 tokens (the reference's cases 2-4: 94 / 92 / 102 us fused against 101 / 97 /
+// 115 layer-wise) and loses from 8192 (case 1: 161 against 147 us); at d_model 256 the layer-wise
+// plan with narrow GEMM tiles is as fast or faster (C1 68 / 68 us, C2 106 against 118 us).
+static constexpr int64_t kFusedLnMaxTokens = 2048;
+static constexpr int kFusedLnMaxDModel = 128;
 
 // The automatic plan only picks a fused plan for shapes its kernels take (64-multiple d_model
 // and ffn_dim; head_dim 32 / 64 for the megakernel); an explicit plan is returned as asked and
@@ -137,8 +137,7 @@ static int resolve_plan(int plan, int B, int S, int D, int H, int F) {
   const bool tiles64 = D % 64 == 0 && F % 64 == 0 && D <= kMegaMaxDModel;
   const int hd = H > 0 ? D / H : 0;
   if (T <= kMegaMaxTokens && tiles64 && (hd == 32 || hd == 64)) return TT_PLAN_MEGAKERNEL;
-  if (tiles64 && (T <= kFusedLnMaxTokens || (D <= 128 && T <= kFusedLnMaxTokensNarrow)))
-    return TT_PLAN_FUSED_LN;
+  if (tiles64 && D <= kFusedLnMaxDModel && T <= kFusedLnMaxTokens) return TT_PLAN_FUSED_LN;
   return TT_PLAN_LAYERWISE;
 }
 

@@ -397,30 +397,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
   }
 }
 
-// Small-shape GEMM for projections whose N or K is not a multiple of 64 (d_model 32 and the
-// like): one thread computes 4 consecutive outputs of one row with fp32 FMAs, 16-byte loads of
-// X and W rows (K % 8 == 0), and the same epilogue semantics as gemm_kernel, element by element.
-// These shapes are a few MFLOP; the MFMA tiles are kept for everything else.
+// Epilogue of 4 consecutive outputs n .. n + 3 of row m from their fp32 sums (the semantics of
+// gemm_kernel's epilogue, element by element), for the small-shape and narrow-tile kernels.
 template <int MODE>
-__global__ __launch_bounds__(256) void gemm_small_kernel(const half* __restrict__ X,
-                                                         const half* __restrict__ W, int M, int N,
-                                                         int K, EpiArgs ep) {
-  const int ngroups = N / 4;
-  const long g = (long)blockIdx.x * 256 + threadIdx.x;
-  if (g >= (long)M * ngroups) return;
-  const int m = (int)(g / ngroups), n = (int)(g - (long)m * ngroups) * 4;
-  const half* xr = X + (size_t)m * K;
-  const half* wr = W + (size_t)n * K;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int k = 0; k < K; k += 8) {
-    const half8 xv = *(const half8*)(xr + k);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const half8 wv = *(const half8*)(wr + (size_t)e * K + k);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) acc[e] = fmaf((float)xv[t], (float)wv[t], acc[e]);
-    }
-  }
+__device__ __forceinline__ void epilogue4(const EpiArgs& ep, int m, int n, const float acc[4]) {
   const bool keep = ep.valid == nullptr || ep.valid[m] != 0;
   half4 hv;
 #pragma unroll
@@ -462,6 +442,33 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const half* __restrict_
   }
 }
 
+// Small-shape GEMM for projections whose N or K is not a multiple of 64 (d_model 32 and the
+// like): one thread computes 4 consecutive outputs of one row with fp32 FMAs, 16-byte loads of
+// X and W rows (K % 8 == 0), and the same epilogue semantics as gemm_kernel, element by element.
+// These shapes are a few MFLOP; the MFMA tiles are kept for everything else.
+template <int MODE>
+__global__ __launch_bounds__(256) void gemm_small_kernel(const half* __restrict__ X,
+                                                         const half* __restrict__ W, int M, int N,
+                                                         int K, EpiArgs ep) {
+  const int ngroups = N / 4;
+  const long g = (long)blockIdx.x * 256 + threadIdx.x;
+  if (g >= (long)M * ngroups) return;
+  const int m = (int)(g / ngroups), n = (int)(g - (long)m * ngroups) * 4;
+  const half* xr = X + (size_t)m * K;
+  const half* wr = W + (size_t)n * K;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < K; k += 8) {
+    const half8 xv = *(const half8*)(xr + k);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const half8 wv = *(const half8*)(wr + (size_t)e * K + k);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[e] = fmaf((float)xv[t], (float)wv[t], acc[e]);
+    }
+  }
+  epilogue4<MODE>(ep, m, n, acc);
+}
+
 static int run_small(int mode, const half* x, const half* w, int m, int n, int k,
                      const EpiArgs& ep, hipStream_t stream) {
   const long threads = (long)m * (n / 4);
@@ -486,6 +493,94 @@ static int run_small(int mode, const half* x, const half* w, int m, int n, int k
       break;
   }
   return launch_status("gemm_small_kernel");
+}
+
+// Narrow-tile GEMM for grids that would leave most CUs idle (few tokens): 32 x 32 output tiles, so
+// four times as many blocks as 64 x 64 tiles pull operands (each CU's streaming rate is set by the
+// bytes it keeps in flight), with the K range split over the block's four waves.  Each wave loads
+// its W and X fragments straight into registers (lane l: row l % 32, 8 K values at 8 (l / 32)),
+// NPF K steps ahead, and accumulates one 32 x 32 MFMA tile; the four partial tiles are summed in
+// LDS in wave order (deterministic) and the epilogue runs 4 outputs per thread.
+constexpr int kNarrow = 32;
+template <int MODE>
+__global__ __launch_bounds__(256) void gemm_narrow_kernel(const half* __restrict__ X,
+                                                          const half* __restrict__ W, int M, int N,
+                                                          int K, EpiArgs ep) {
+  constexpr int NPF = 4;  // K steps of 16 per register buffer
+  const int tiles_n = N / kNarrow;
+  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  const int m0 = tm * kNarrow, n0 = tn * kNarrow;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, kh = 8 * (lane >> 5);
+  const half* xr = X + (size_t)min(m0 + r, M - 1) * K + kh;
+  const half* wr = W + (size_t)(n0 + r) * K + kh;
+  const int steps = K / 16 / 4;          // K steps of this wave (K % 64 == 0)
+  const int kbeg = wave * steps * 16;
+  floatx16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  half8 a[2][NPF], b[2][NPF];
+  auto load = [&](int buf, int s0) {
+#pragma unroll
+    for (int j = 0; j < NPF; ++j) {
+      const int k = kbeg + 16 * min(s0 + j, steps - 1);  // past the end: reload the last step
+      a[buf][j] = *(const half8*)(wr + k);
+      b[buf][j] = *(const half8*)(xr + k);
+    }
+  };
+  auto mma = [&](int buf, int s0) {
+#pragma unroll
+    for (int j = 0; j < NPF; ++j)
+      if (s0 + j < steps) acc = mfma32x32x16(a[buf][j], b[buf][j], acc);
+  };
+  // Two buffers, alternated by a loop unrolled twice (register arrays need compile-time indices).
+  load(0, 0);
+  for (int s0 = 0; s0 < steps; s0 += 2 * NPF) {
+    if (s0 + NPF < steps) load(1, s0 + NPF);
+    mma(0, s0);
+    if (s0 + NPF >= steps) break;
+    if (s0 + 2 * NPF < steps) load(0, s0 + 2 * NPF);
+    mma(1, s0 + NPF);
+  }
+  // acc[4g + e] = C[m0 + r][n0 + 8g + 4 (lane / 32) + e]
+  __shared__ __align__(16) float part[4][kNarrow][kNarrow];
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+    *(floatx4*)&part[wave][r][8 * g + 4 * (lane >> 5)] =
+        floatx4{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
+  __syncthreads();
+  const int ml = threadIdx.x >> 3, nl = 4 * (threadIdx.x & 7);
+  if (m0 + ml >= M) return;
+  float sum[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    sum[e] = ((part[0][ml][nl + e] + part[1][ml][nl + e]) + part[2][ml][nl + e]) + part[3][ml][nl + e];
+  epilogue4<MODE>(ep, m0 + ml, n0 + nl, sum);
+}
+
+static int run_narrow(int mode, const half* x, const half* w, int m, int n, int k,
+                      const EpiArgs& ep, hipStream_t stream) {
+  const long blocks = (long)((m + kNarrow - 1) / kNarrow) * (n / kNarrow);
+  TT_REQUIRE(blocks < (1L << 31), "linear: grid too large");
+  const dim3 grid((unsigned)blocks), block(256);
+  switch (mode) {
+    case TT_EPI_BIAS:
+      hipLaunchKernelGGL(gemm_narrow_kernel<TT_EPI_BIAS>, grid, block, 0, stream, x, w, m, n, k, ep);
+      break;
+    case TT_EPI_BIAS_GELU:
+      hipLaunchKernelGGL(gemm_narrow_kernel<TT_EPI_BIAS_GELU>, grid, block, 0, stream, x, w, m, n, k, ep);
+      break;
+    case TT_EPI_RESID_MASKED:
+      hipLaunchKernelGGL(gemm_narrow_kernel<TT_EPI_RESID_MASKED>, grid, block, 0, stream, x, w, m, n, k, ep);
+      break;
+    case TT_EPI_MASKED_RESID:
+      hipLaunchKernelGGL(gemm_narrow_kernel<TT_EPI_MASKED_RESID>, grid, block, 0, stream, x, w, m, n, k, ep);
+      break;
+    default:
+      hipLaunchKernelGGL(gemm_narrow_kernel<TT_EPI_QKV>, grid, block, 0, stream, x, w, m, n, k, ep);
+      break;
+  }
+  return launch_status("gemm_narrow_kernel");
 }
 
 // ---- host-side tile selection ----
@@ -524,7 +619,8 @@ static int run_mode(int tile, const half* x, const half* w, int m, int n, int k,
   }
 }
 
-static const TileCfg kTiles[] = {{256, 256}, {256, 128}, {128, 128}, {128, 64}, {64, 64}};
+// index 5: 32 x 32 narrow tiles (gemm_narrow_kernel), chosen for grids that leave most CUs idle
+static const TileCfg kTiles[] = {{256, 256}, {256, 128}, {128, 128}, {128, 64}, {64, 64}, {32, 32}};
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
 static int g_tile_override = -1;  // test hook: force one tile configuration
@@ -533,15 +629,20 @@ static int g_tile_override = -1;  // test hook: force one tile configuration
 // 4096, 8192}): a 256x256 block (one per CU, 128 KiB of LDS) only pays off once K is long enough
 // to amortise its prologue and its 128 KiB epilogue (K >= 4096) and the grid still fills every CU;
 // otherwise 128x128 (two blocks per CU, so one block's epilogue overlaps the other's MFMAs) is
-// the fastest shape.  Narrower tiles are used when a wider one would leave CUs idle.
+// the fastest shape.  Narrower tiles are used when a wider one would leave CUs idle, down to the
+// 32x32 narrow kernel for few-token grids.
 static int pick_tile(int m, int n, int k, int cus) {
   if (g_tile_override >= 0 && g_tile_override < kNumTiles && n % kTiles[g_tile_override].bn == 0)
     return g_tile_override;
   auto tiles = [&](int i) { return (long)((m + kTiles[i].bm - 1) / kTiles[i].bm) * (n / kTiles[i].bn); };
   if (k >= 4096 && n % 256 == 0 && tiles(0) >= cus) return 0;
-  for (int i = 2; i < kNumTiles; ++i)
+  for (int i = 2; i < 4; ++i)
     if (n % kTiles[i].bn == 0 && tiles(i) >= cus) return i;
-  return kNumTiles - 1;  // 64x64: every N that is a multiple of 64
+  // Few tokens: 64 x 64 tiles that would fill at most half the CUs become 32 x 32 narrow tiles
+  // (measured on MI355X: C1 77 -> 68 us, C2 138 -> 106 us; C1 / C2 ffn_out has 32 / 4 tiles of
+  // K = 1024 at 64 x 64, 10-11 us, each CU limited by the bytes it keeps in flight).
+  if (2 * tiles(4) <= cus) return 5;
+  return 4;  // 64x64: every N that is a multiple of 64
 }
 
 static int device_cus() {
@@ -580,6 +681,7 @@ int launch_linear(const half* x, const half* w, int m, int n, int k, const EpiAr
   if (m == 0) return TT_OK;
   if (k % kBK != 0 || n % 64 != 0) return run_small(ep.mode, x, w, m, n, k, ep, stream);
   const int tile = pick_tile(m, n, k, device_cus());
+  if (tile == 5) return run_narrow(ep.mode, x, w, m, n, k, ep, stream);
   switch (ep.mode) {
     case TT_EPI_BIAS: return run_mode<TT_EPI_BIAS>(tile, x, w, m, n, k, ep, stream);
     case TT_EPI_BIAS_GELU: return run_mode<TT_EPI_BIAS_GELU>(tile, x, w, m, n, k, ep, stream);
