@@ -74,6 +74,13 @@ __device__ __forceinline__ void raw_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Barrier after this wave's LDS operations have completed (s_waitcnt lgkmcnt(0), vector-memory
+// loads left in flight): for pipelines whose global loads run several stages ahead in registers.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt 63, expcnt 7, lgkmcnt 0
+  raw_barrier();
+}
+
 // Global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane l writes LDS bytes
 // [16 l, 16 l + 16) after the wave-uniform destination `lds_dst`.
 __device__ __forceinline__ void lds_copy16(const half* src, half* lds_dst) {

@@ -18,6 +18,7 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -131,7 +132,18 @@ __device__ void fill_padded_tile(const EpiArgs& ep, int M, int m0, int n0) {
 // applied on the global side: lane l fetches logical chunk (l % 8) ^ (l / 8) of its row, so the
 // physical chunk of logical chunk c in row r is c ^ (r % 8), as swz() expects.
 
-template <int BM, int BN, int MODE>
+// Register-path staging (PATH = 1): each thread moves 16-byte chunks global -> VGPR -> LDS with
+// buffer loads and ds_write_b128, two K stages ahead in two register sets, so a CU keeps three K
+// stages of operands in flight instead of one.  That is what a grid of about one tile per CU
+// streaming a long K needs (its time is the latency of the bytes each CU has in flight); with
+// several tiles per CU the direct global -> LDS copies (PATH = 0) are as fast.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const half* base, int bytes) {
+  // raw buffer: stride 0, num_records = bytes; 0x00020000 is the gfx9 data-format word for
+  // untyped 32-bit accesses
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, bytes, 0x00020000);
+}
+
+template <int BM, int BN, int MODE, int PATH>
 __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
                                                    const half* __restrict__ W, int M, int N, int K,
                                                    EpiArgs ep) {
@@ -168,25 +180,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
     }
   }
 
-  // Copy sources: copy i of this wave fills 8-row group wave + 4 i of the stage.  X rows past M
-  // are clamped to M - 1 (valid memory whose results are never stored).
-  // Offsets are relative to the block's first X row and W row (64-bit bases), so M * K may
-  // exceed 2^31 (long sequences); BM * K and BN * K stay far below it.
-  const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
-  const half* Xb = X + (size_t)m0 * K;
-  const half* Wb = W + (size_t)n0 * K;
-  int src_off[NL];
-#pragma unroll
-  for (int i = 0; i < NL; ++i) {
-    const int r = (wave + 4 * i) * 8 + lrow;
-    if (i < XL) src_off[i] = min(r, M - 1 - m0) * K + lchunk * 8;
-    else src_off[i] = (r - BM) * K + lchunk * 8;
-  }
-  auto copy = [&](int i, int k0, half* stage) {
-    const half* base = (i < XL) ? Xb : Wb;
-    lds_copy16(base + src_off[i] + k0, stage + (wave + 4 * i) * 8 * kBK);
-  };
-
   floatx16 acc[FN][FM];
 #pragma unroll
   for (int i = 0; i < FN; ++i)
@@ -214,60 +207,170 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
       bf[buf][j] = *(const half8*)(stage + (wm * WM + j * 32 + frow) * kBK + pc * 8);
   };
 
-  // One stage: KSUB k-steps of FN x FM MFMAs.  Fragment reads for k-step kk + 1 and (MORE) the
-  // copies of the next stage are interleaved one per MFMA.
-  auto stage = [&](auto more_tag, const half* cur, half* nxt, int k1) {
-    constexpr bool MORE = decltype(more_tag)::value;
-    frags(0, 0, cur);
+  if constexpr (PATH == 0) {
+    // Copy sources: copy i of this wave fills 8-row group wave + 4 i of the stage.  X rows past M
+    // are clamped to M - 1 (valid memory whose results are never stored).
+    // Offsets are relative to the block's first X row and W row (64-bit bases), so M * K may
+    // exceed 2^31 (long sequences); BM * K and BN * K stay far below it.
+    const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
+    const half* Xb = X + (size_t)m0 * K;
+    const half* Wb = W + (size_t)n0 * K;
+    int src_off[NL];
 #pragma unroll
-    for (int kk = 0; kk < KSUB; ++kk) {
-      __builtin_amdgcn_sched_barrier(0);
-      if (kk + 1 < KSUB) frags((kk + 1) & 1, kk + 1, cur);
-      // The next stage's copies go out during the first CSPREAD k-steps, so they have most of
-      // the stage to land before the end-of-stage wait.
-      const int c_lo = kk < CSPREAD ? kk * NL / CSPREAD : NL;
-      const int c_hi = kk < CSPREAD ? (kk + 1) * NL / CSPREAD : NL;
-      if constexpr (MORE) {
-#pragma unroll
-        for (int c = c_lo; c < c_hi; ++c) copy(c, k1, nxt);
-      }
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-#pragma unroll
-        for (int j = 0; j < FM; ++j)
-          acc[i][j] = mfma32x32x16(af[kk & 1][i], bf[kk & 1][j], acc[i][j]);
-      if (kk + 1 < KSUB) {
-#pragma unroll
-        for (int t = 0; t < FN + FM; ++t) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-      }
-      if constexpr (MORE) {
-#pragma unroll
-        for (int c = c_lo; c < c_hi; ++c) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        }
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, FN * FM, 0);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < NL; ++i) {
+      const int r = (wave + 4 * i) * 8 + lrow;
+      if (i < XL) src_off[i] = min(r, M - 1 - m0) * K + lchunk * 8;
+      else src_off[i] = (r - BM) * K + lchunk * 8;
     }
-  };
+    auto copy = [&](int i, int k0, half* stage) {
+      const half* base = (i < XL) ? Xb : Wb;
+      lds_copy16(base + src_off[i] + k0, stage + (wave + 4 * i) * 8 * kBK);
+    };
 
-  const int nk = K / kBK;
-  // Prologue: stage 0.
+    // One stage: KSUB k-steps of FN x FM MFMAs.  Fragment reads for k-step kk + 1 and (MORE) the
+    // copies of the next stage are interleaved one per MFMA.
+    auto stage = [&](auto more_tag, const half* cur, half* nxt, int k1) {
+      constexpr bool MORE = decltype(more_tag)::value;
+      frags(0, 0, cur);
 #pragma unroll
-  for (int i = 0; i < NL; ++i) copy(i, 0, lds);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk - 1; ++kt) {
-    stage(std::true_type{}, lds + (kt & 1) * STAGE, lds + ((kt + 1) & 1) * STAGE, (kt + 1) * kBK);
-    // The next stage's copies have landed in LDS and every wave is done reading this stage.
+      for (int kk = 0; kk < KSUB; ++kk) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (kk + 1 < KSUB) frags((kk + 1) & 1, kk + 1, cur);
+        // The next stage's copies go out during the first CSPREAD k-steps, so they have most of
+        // the stage to land before the end-of-stage wait.
+        const int c_lo = kk < CSPREAD ? kk * NL / CSPREAD : NL;
+        const int c_hi = kk < CSPREAD ? (kk + 1) * NL / CSPREAD : NL;
+        if constexpr (MORE) {
+#pragma unroll
+          for (int c = c_lo; c < c_hi; ++c) copy(c, k1, nxt);
+        }
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+          for (int j = 0; j < FM; ++j)
+            acc[i][j] = mfma32x32x16(af[kk & 1][i], bf[kk & 1][j], acc[i][j]);
+        if (kk + 1 < KSUB) {
+#pragma unroll
+          for (int t = 0; t < FN + FM; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+        }
+        if constexpr (MORE) {
+#pragma unroll
+          for (int c = c_lo; c < c_hi; ++c) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+          }
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, FN * FM, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+
+    const int nk = K / kBK;
+    // Prologue: stage 0.
+#pragma unroll
+    for (int i = 0; i < NL; ++i) copy(i, 0, lds);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    for (int kt = 0; kt < nk - 1; ++kt) {
+      stage(std::true_type{}, lds + (kt & 1) * STAGE, lds + ((kt + 1) & 1) * STAGE, (kt + 1) * kBK);
+      // The next stage's copies have landed in LDS and every wave is done reading this stage.
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    stage(std::false_type{}, lds + ((nk - 1) & 1) * STAGE, nullptr, 0);
+
+  } else {
+    // Register path.  Thread t moves chunk t % 8 of rows t / 8 + 32 i (i < RX: X rows, then W
+    // rows) of every stage.  The buffers start at the block's first X / W row, so offsets stay
+    // below BM * K and BN * K; X rows past M are clamped to M - 1 (valid memory whose results are
+    // never stored), so no load depends on the buffer's range check.
+    constexpr int RL = (BM + BN) / 32;   // 16-byte chunks per thread per stage
+    constexpr int RX = BM / 32;
+    const int tid = threadIdx.x;
+    const int lr = tid >> 3, lc = tid & 7;
+    // The tile origin is wave-uniform; readfirstlane states it, so the buffer descriptors live in
+    // SGPRs (after the padded-tile early return the compiler cannot prove it, and a descriptor in
+    // VGPRs turns every load into a waterfall loop).
+    const int m0u = __builtin_amdgcn_readfirstlane(m0), n0u = __builtin_amdgcn_readfirstlane(n0);
+    const int xrows = min(M - m0u, BM);
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X + (size_t)m0u * K, xrows * K * 2);
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(W + (size_t)n0u * K, BN * K * 2);
+    int roff[RL];  // byte offset of the thread's chunk in K stage 0
+#pragma unroll
+    for (int i = 0; i < RL; ++i) {
+      const int r = i < RX ? min(lr + 32 * i, xrows - 1) : lr + 32 * (i - RX);
+      roff[i] = (r * K + lc * 8) * 2;
+    }
+    const int dst0 = lr * kBK + swz(lr, lc) * 8;  // rows lr + 32 i share lr's swizzle
+    const int nk = K / kBK;
+    // chunk i of K stage kt (stages past the end re-read the last one; never used)
+    auto ld = [&](int i, int kt) -> u32x4 {
+      const int kb = min(kt, nk - 1) * (kBK * 2);
+      return __builtin_amdgcn_raw_buffer_load_b128(i < RX ? xr : wr, roff[i] + kb, 0, 0);
+    };
+    u32x4 sa[RL], sb[RL];
+#pragma unroll
+    for (int i = 0; i < RL; ++i) sa[i] = ld(i, 0);
+#pragma unroll
+    for (int i = 0; i < RL; ++i) sb[i] = ld(i, 1);
+#pragma unroll
+    for (int i = 0; i < RL; ++i) {
+      *(u32x4*)(lds + dst0 + i * 32 * kBK) = sa[i];
+      sa[i] = ld(i, 2);
+    }
+    lds_barrier();
+    // Stage kt: MFMAs on LDS buffer kt % 2; the chunks of stage kt + 1 (in S) go to the other
+    // buffer during the first two k-steps, each followed by the load of stage kt + 3 into its
+    // register.  The body has no branches, so the MFMAs, fragment reads, LDS writes and loads
+    // interleave one per MFMA.
+    auto body = [&](int kt, u32x4 (&S)[RL]) {
+      const half* cur = lds + (kt & 1) * STAGE;
+      half* nxt = lds + ((kt + 1) & 1) * STAGE;
+      frags(0, 0, cur);
+#pragma unroll
+      for (int kk = 0; kk < KSUB; ++kk) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (kk + 1 < KSUB) frags((kk + 1) & 1, kk + 1, cur);
+        constexpr int PER = (RL + 1) / 2;
+        const int lo = kk < 2 ? kk * PER : RL, hi = kk < 2 ? min(RL, (kk + 1) * PER) : RL;
+#pragma unroll
+        for (int i = lo; i < hi; ++i) {
+          *(u32x4*)(nxt + dst0 + i * 32 * kBK) = S[i];
+          S[i] = ld(i, kt + 3);
+        }
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+          for (int j = 0; j < FM; ++j)
+            acc[i][j] = mfma32x32x16(af[kk & 1][i], bf[kk & 1][j], acc[i][j]);
+        if (kk + 1 < KSUB) {
+#pragma unroll
+          for (int t = 0; t < FN + FM; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+        }
+#pragma unroll
+        for (int t = lo; t < hi; ++t) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, FN * FM, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      lds_barrier();
+    };
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+      body(kt, sb);
+      body(kt + 1, sa);
+    }
+    if (kt < nk) body(kt, sb);
   }
-  stage(std::false_type{}, lds + ((nk - 1) & 1) * STAGE, nullptr, 0);
 
   // ---- Epilogue ----
   // acc[i][j][4g+e] = C[m][n] with m = row j*32 + lane%32 of the wave tile and
@@ -588,22 +691,23 @@ struct TileCfg {
   int bm, bn;
 };
 
-template <int BM, int BN, int MODE>
+template <int BM, int BN, int MODE, int PATH>
 static int run_tile(const half* x, const half* w, int m, int n, int k, const EpiArgs& ep,
                     hipStream_t stream) {
   constexpr int NT = 256;
-  const size_t lds = 2 * (size_t)(BM + BN) * kBK * sizeof(half);
+  // double-buffered K stages; the epilogue stages the whole BM x BN tile in the same memory
+  const size_t lds = std::max(2 * (size_t)(BM + BN) * kBK, (size_t)BM * BN) * sizeof(half);
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
   std::call_once(once, [&] {
-    attr_err = hipFuncSetAttribute((const void*)gemm_kernel<BM, BN, MODE>,
+    attr_err = hipFuncSetAttribute((const void*)gemm_kernel<BM, BN, MODE, PATH>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   });
   if (attr_err != hipSuccess)
     return fail(TT_ERR_HIP, "hipFuncSetAttribute(gemm %dx%d): %s", BM, BN, hipGetErrorString(attr_err));
   const int tiles = ((m + BM - 1) / BM) * (n / BN);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, MODE>), dim3(tiles), dim3(NT), lds, stream, x, w, m, n,
-                     k, ep);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, MODE, PATH>), dim3(tiles), dim3(NT), lds, stream, x, w,
+                     m, n, k, ep);
   return launch_status("gemm_kernel");
 }
 
@@ -611,16 +715,21 @@ template <int MODE>
 static int run_mode(int tile, const half* x, const half* w, int m, int n, int k, const EpiArgs& ep,
                     hipStream_t stream) {
   switch (tile) {
-    case 0: return run_tile<256, 256, MODE>(x, w, m, n, k, ep, stream);
-    case 1: return run_tile<256, 128, MODE>(x, w, m, n, k, ep, stream);
-    case 2: return run_tile<128, 128, MODE>(x, w, m, n, k, ep, stream);
-    case 3: return run_tile<128, 64, MODE>(x, w, m, n, k, ep, stream);
-    default: return run_tile<64, 64, MODE>(x, w, m, n, k, ep, stream);
+    case 0: return run_tile<256, 256, MODE, 0>(x, w, m, n, k, ep, stream);
+    case 1: return run_tile<256, 128, MODE, 0>(x, w, m, n, k, ep, stream);
+    case 2: return run_tile<128, 128, MODE, 0>(x, w, m, n, k, ep, stream);
+    case 3: return run_tile<128, 64, MODE, 0>(x, w, m, n, k, ep, stream);
+    case 6: return run_tile<128, 256, MODE, 1>(x, w, m, n, k, ep, stream);
+    case 7: return run_tile<128, 128, MODE, 1>(x, w, m, n, k, ep, stream);
+    case 8: return run_tile<128, 64, MODE, 1>(x, w, m, n, k, ep, stream);
+    default: return run_tile<64, 64, MODE, 0>(x, w, m, n, k, ep, stream);
   }
 }
 
-// index 5: 32 x 32 narrow tiles (gemm_narrow_kernel), chosen for grids that leave most CUs idle
-static const TileCfg kTiles[] = {{256, 256}, {256, 128}, {128, 128}, {128, 64}, {64, 64}, {32, 32}};
+// index 5: 32 x 32 narrow tiles (gemm_narrow_kernel), chosen for grids that leave most CUs idle;
+// indices 6-8: 128 x 256, 128 x 128, 128 x 64 on the register path
+static const TileCfg kTiles[] = {{256, 256}, {256, 128}, {128, 128}, {128, 64}, {64, 64},
+                                 {32, 32},   {128, 256}, {128, 128}, {128, 64}};
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
 static int g_tile_override = -1;  // test hook: force one tile configuration
@@ -636,8 +745,12 @@ static int pick_tile(int m, int n, int k, int cus) {
     return g_tile_override;
   auto tiles = [&](int i) { return (long)((m + kTiles[i].bm - 1) / kTiles[i].bm) * (n / kTiles[i].bn); };
   if (k >= 4096 && n % 256 == 0 && tiles(0) >= cus) return 0;
+  // One round of 128 x 64 tiles streaming a long K is latency-bound: each CU moves only the bytes
+  // it keeps in flight, and the register path keeps two more K stages in flight than the direct
+  // copies (measured on MI355X, 4096 x 512 x 2048: 22.3 -> 15.8 us).  On grids of several tiles
+  // per CU the direct path is as fast or faster (M = 8192 projections), so it stays there.
   for (int i = 2; i < 4; ++i)
-    if (n % kTiles[i].bn == 0 && tiles(i) >= cus) return i;
+    if (n % kTiles[i].bn == 0 && tiles(i) >= cus) return (i == 3 && k >= 1024) ? 8 : i;
   // Few tokens: 64 x 64 tiles that would fill at most half the CUs become 32 x 32 narrow tiles
   // (measured on MI355X: C1 77 -> 68 us, C2 138 -> 106 us; C1 / C2 ffn_out has 32 / 4 tiles of
   // K = 1024 at 64 x 64, 10-11 us, each CU limited by the bytes it keeps in flight).
