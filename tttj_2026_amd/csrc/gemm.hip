@@ -151,7 +151,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int FM = WM / 32, FN = WN / 32;
   constexpr int ROWS = BM + BN;       // LDS rows per stage: X rows [0, BM), W rows [BM, BM + BN)
-  constexpr int STAGE = ROWS * kBK;   // halfs per stage
+  // LDS row stride in halfs: 128-byte rows with XOR-swizzled chunks for the direct copies (one
+  // copy instruction fills 1 KiB contiguously, so rows cannot be padded); rows padded to 144 bytes
+  // on the register path, which leaves the 16 rows one ds_read_b128 phase reads in 16 different
+  // bank groups (the XOR swizzle covers only 8: rows r and r + 8 share banks).
+  constexpr int LDR = PATH ? kBK + 8 : kBK;
+  constexpr int STAGE = ROWS * LDR;   // halfs per stage
   constexpr int XL = BM / 32;         // X copies per wave per stage (8 rows x 4 waves each)
   constexpr int WL = BN / 32;         // W copies per wave per stage
   constexpr int NL = XL + WL;
@@ -198,13 +203,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
   const int frow = lane & 31, fhi = lane >> 5, fx = lane & 7;
   half8 af[2][FN], bf[2][FM];
   auto frags = [&](int buf, int kk, const half* stage) {
-    const int pc = (2 * kk + fhi) ^ fx;
+    const int pc = PATH ? 2 * kk + fhi : (2 * kk + fhi) ^ fx;
 #pragma unroll
     for (int i = 0; i < FN; ++i)
-      af[buf][i] = *(const half8*)(stage + (BM + wn * WN + i * 32 + frow) * kBK + pc * 8);
+      af[buf][i] = *(const half8*)(stage + (BM + wn * WN + i * 32 + frow) * LDR + pc * 8);
 #pragma unroll
     for (int j = 0; j < FM; ++j)
-      bf[buf][j] = *(const half8*)(stage + (wm * WM + j * 32 + frow) * kBK + pc * 8);
+      bf[buf][j] = *(const half8*)(stage + (wm * WM + j * 32 + frow) * LDR + pc * 8);
   };
 
   if constexpr (PATH == 0) {
@@ -304,7 +309,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
       const int r = i < RX ? min(lr + 32 * i, xrows - 1) : lr + 32 * (i - RX);
       roff[i] = (r * K + lc * 8) * 2;
     }
-    const int dst0 = lr * kBK + swz(lr, lc) * 8;  // rows lr + 32 i share lr's swizzle
+    const int dst0 = lr * LDR + lc * 8;
     const int nk = K / kBK;
     // chunk i of K stage kt (stages past the end re-read the last one; never used)
     auto ld = [&](int i, int kt) -> u32x4 {
@@ -318,7 +323,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
     for (int i = 0; i < RL; ++i) sb[i] = ld(i, 1);
 #pragma unroll
     for (int i = 0; i < RL; ++i) {
-      *(u32x4*)(lds + dst0 + i * 32 * kBK) = sa[i];
+      *(u32x4*)(lds + dst0 + i * 32 * LDR) = sa[i];
       sa[i] = ld(i, 2);
     }
     lds_barrier();
@@ -338,7 +343,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
         const int lo = kk < 2 ? kk * PER : RL, hi = kk < 2 ? min(RL, (kk + 1) * PER) : RL;
 #pragma unroll
         for (int i = lo; i < hi; ++i) {
-          *(u32x4*)(nxt + dst0 + i * 32 * kBK) = S[i];
+          *(u32x4*)(nxt + dst0 + i * 32 * LDR) = S[i];
           S[i] = ld(i, kt + 3);
         }
 #pragma unroll
@@ -696,7 +701,8 @@ static int run_tile(const half* x, const half* w, int m, int n, int k, const Epi
                     hipStream_t stream) {
   constexpr int NT = 256;
   // double-buffered K stages; the epilogue stages the whole BM x BN tile in the same memory
-  const size_t lds = std::max(2 * (size_t)(BM + BN) * kBK, (size_t)BM * BN) * sizeof(half);
+  const size_t lds = std::max(2 * (size_t)(BM + BN) * (PATH ? kBK + 8 : kBK), (size_t)BM * BN) *
+                     sizeof(half);
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
   std::call_once(once, [&] {
@@ -722,14 +728,15 @@ static int run_mode(int tile, const half* x, const half* w, int m, int n, int k,
     case 6: return run_tile<128, 256, MODE, 1>(x, w, m, n, k, ep, stream);
     case 7: return run_tile<128, 128, MODE, 1>(x, w, m, n, k, ep, stream);
     case 8: return run_tile<128, 64, MODE, 1>(x, w, m, n, k, ep, stream);
+    case 9: return run_tile<256, 128, MODE, 1>(x, w, m, n, k, ep, stream);
     default: return run_tile<64, 64, MODE, 0>(x, w, m, n, k, ep, stream);
   }
 }
 
 // index 5: 32 x 32 narrow tiles (gemm_narrow_kernel), chosen for grids that leave most CUs idle;
-// indices 6-8: 128 x 256, 128 x 128, 128 x 64 on the register path
+// indices 6-9: 128 x 256, 128 x 128, 128 x 64, 256 x 128 on the register path
 static const TileCfg kTiles[] = {{256, 256}, {256, 128}, {128, 128}, {128, 64}, {64, 64},
-                                 {32, 32},   {128, 256}, {128, 128}, {128, 64}};
+                                 {32, 32},   {128, 256}, {128, 128}, {128, 64}, {256, 128}};
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
 static int g_tile_override = -1;  // test hook: force one tile configuration
@@ -740,11 +747,18 @@ static int g_tile_override = -1;  // test hook: force one tile configuration
 // otherwise 128x128 (two blocks per CU, so one block's epilogue overlaps the other's MFMAs) is
 // the fastest shape.  Narrower tiles are used when a wider one would leave CUs idle, down to the
 // 32x32 narrow kernel for few-token grids.
-static int pick_tile(int m, int n, int k, int cus) {
+static int pick_tile(int m, int n, int k, int mode, int cus) {
   if (g_tile_override >= 0 && g_tile_override < kNumTiles && n % kTiles[g_tile_override].bn == 0)
     return g_tile_override;
   auto tiles = [&](int i) { return (long)((m + kTiles[i].bm - 1) / kTiles[i].bm) * (n / kTiles[i].bn); };
   if (k >= 4096 && n % 256 == 0 && tiles(0) >= cus) return 0;
+  // Register-path tiles with padded LDS rows, where they measured ahead of the direct copies
+  // (MI355X, M = 8192, medians of interleaved runs): 256 x 128 for one round of tiles with
+  // K >= 4096 (N = 1024: 77.5 -> 75.1 us) and 128 x 128 for the GELU epilogue (N = 4096, K = 1024:
+  // 101.5 -> 96.7 us; two blocks per CU overlap one block's GELU with the other's MFMAs).  For
+  // the other M = 8192 projections the two paths tie.
+  if (k >= 4096 && n % 128 == 0 && tiles(9) >= cus) return 9;
+  if (mode == TT_EPI_BIAS_GELU && n % 128 == 0 && tiles(7) >= cus) return 7;
   // One round of 128 x 64 tiles streaming a long K is latency-bound: each CU moves only the bytes
   // it keeps in flight, and the register path keeps two more K stages in flight than the direct
   // copies (measured on MI355X, 4096 x 512 x 2048: 22.3 -> 15.8 us).  On grids of several tiles
@@ -793,7 +807,7 @@ int launch_linear(const half* x, const half* w, int m, int n, int k, const EpiAr
   }
   if (m == 0) return TT_OK;
   if (k % kBK != 0 || n % 64 != 0) return run_small(ep.mode, x, w, m, n, k, ep, stream);
-  const int tile = pick_tile(m, n, k, device_cus());
+  const int tile = pick_tile(m, n, k, ep.mode, device_cus());
   if (tile == 5) return run_narrow(ep.mode, x, w, m, n, k, ep, stream);
   switch (ep.mode) {
     case TT_EPI_BIAS: return run_mode<TT_EPI_BIAS>(tile, x, w, m, n, k, ep, stream);
