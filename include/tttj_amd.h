@@ -69,8 +69,8 @@ int tt_weight_layout(int d_model, int ffn_dim, int num_layers, int64_t layer_off
                      int64_t* layer_stride, int64_t* final_norm_offset, int64_t* total_elems);
 
 /* Execution plans of tt_transformer_fwd. */
-#define TT_PLAN_AUTO 0       /* fused-LN layer-wise plan for few tokens and d_model <= 512, else
-                              * layer-wise */
+#define TT_PLAN_AUTO 0       /* fused-LN layer-wise plan for d_model <= 128 and at most 2048
+                              * tokens, else layer-wise */
 #define TT_PLAN_LAYERWISE 1  /* one launch per op: LN, GEMMs with fused epilogues, attention */
 #define TT_PLAN_MEGAKERNEL 2 /* one persistent launch (<= one workgroup per CU) for the stack */
 #define TT_PLAN_FUSED_LN 3   /* layer-wise with LN1 / LN2 computed inside the QKV / ffn_in GEMM
