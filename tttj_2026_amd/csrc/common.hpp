@@ -118,25 +118,28 @@ __device__ __forceinline__ float wave_sum(float v) { return seg_sum<64>(v); }
 
 __device__ __forceinline__ float gelu_erf(float v) {
   // Exact-erf GELU, F.gelu(approximate="none"): v * Phi(v), Phi(v) = erfc(-v / sqrt 2) / 2.
-  // erfc(z), z = |v| / sqrt 2, is t * exp(-z^2 + P(t)) with t = 1 / (1 + z/2) and P a degree-9
-  // polynomial fitted at Chebyshev nodes (the form of Numerical Recipes 6.2; coefficients derived
-  // by fit_erfc.py), relative error < 1e-7 for all z.  Phi(v) = 1 - q for v >= 0 and q for v < 0
-  // with q = erfc(z) / 2, so the result is branch-free and keeps full relative accuracy in the
-  // negative tail: the fp16 result is the correctly rounded GELU except within ~1e-7 of a tie.
-  const float z = fabsf(v) * 0.70710678118654752f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
-  float p = 1.784814059e-01f;
-  p = fmaf(p, t, -8.587818905e-01f);
-  p = fmaf(p, t, 1.562995793e+00f);
-  p = fmaf(p, t, -1.218379551e+00f);
-  p = fmaf(p, t, 3.344113965e-01f);
-  p = fmaf(p, t, -2.089165053e-01f);
-  p = fmaf(p, t, 1.022820283e-01f);
-  p = fmaf(p, t, 3.733488146e-01f);
-  p = fmaf(p, t, 1.000071867e+00f);
-  p = fmaf(p, t, -1.265513274e+00f);
-  const float q = 0.5f * t * __builtin_amdgcn_exp2f((p - z * z) * 1.4426950408889634f);
-  return v * (v >= 0.f ? 1.0f - q : q);
+  // With z = |v| / sqrt 2, erfc(z) = t * exp(-z^2 + P(t)), t = 1 / (1 + z/2) and P a degree-9
+  // polynomial fitted at Chebyshev nodes (the form of Numerical Recipes 6.2; fit_erfc.py derives
+  // the coefficients), relative error < 1e-7 for all z.  Evaluated in the exp2 domain:
+  // w = |v| sqrt(log2(e) / 2), q = erfc(z) / 2 = t * exp2(Q(t) - w^2) with Q = log2(e) P - 1, and
+  // since Phi(v) = 1 - q for v >= 0 and q for v < 0, GELU(v) = max(v, 0) - |v| q for either sign:
+  // branch-free, full relative accuracy in the negative tail, 17 VALU operations.  The fp16 result
+  // is the correctly rounded GELU except within ~1e-7 of a rounding tie.
+  const float a = fabsf(v);
+  const float w = a * 8.493218003e-01f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(w, 4.162773056e-01f, 1.0f));
+  float p = 2.574942392e-01f;
+  p = fmaf(p, t, -1.238960375e+00f);
+  p = fmaf(p, t, 2.254926280e+00f);
+  p = fmaf(p, t, -1.757750137e+00f);
+  p = fmaf(p, t, 4.824536634e-01f);
+  p = fmaf(p, t, -3.014028061e-01f);
+  p = fmaf(p, t, 1.475617750e-01f);
+  p = fmaf(p, t, 5.386284833e-01f);
+  p = fmaf(p, t, 1.442798723e+00f);
+  p = fmaf(p, t, -2.825749725e+00f);
+  const float q = t * __builtin_amdgcn_exp2f(fmaf(-w, w, p));
+  return fmaf(-a, q, fmaxf(v, 0.f));
 }
 
 // 16-byte element chunk index swizzle for [rows][64 halfs] LDS tiles (128-byte rows): XOR with the
