@@ -26,13 +26,23 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const half* __restrict__
     for (int c = lane; c < nch; c += 64) *(uint4*)(y + base + 8 * c) = make_uint4(0, 0, 0, 0);
     return;
   }
-  half8 v[NV];
-  float s = 0.f;
+  // The row and the affine chunks are loaded together, so gamma / beta do not add a memory round
+  // trip after the reductions (the kernel is latency-bound for small row counts).
+  half8 v[NV], g[NV], bt[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + 64 * i;
     if (c < nch) {
       v[i] = *(const half8*)(x + base + 8 * c);
+      g[i] = *(const half8*)(gamma + 8 * c);
+      bt[i] = *(const half8*)(beta + 8 * c);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nch) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) s += (float)v[i][e];
     }
@@ -55,12 +65,10 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const half* __restrict__
   for (int i = 0; i < NV; ++i) {
     const int c = lane + 64 * i;
     if (c < nch) {
-      const half8 g = *(const half8*)(gamma + 8 * c);
-      const half8 b = *(const half8*)(beta + 8 * c);
       half8 o;
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        o[e] = (half)(((float)v[i][e] - mean) * rstd * (float)g[e] + (float)b[e]);
+        o[e] = (half)(((float)v[i][e] - mean) * rstd * (float)g[i][e] + (float)bt[i][e]);
       *(half8*)(y + base + 8 * c) = o;
     }
   }
