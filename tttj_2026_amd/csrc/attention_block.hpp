@@ -37,14 +37,20 @@ __device__ __forceinline__ int pi23(int r) {  // swap bits 2 and 3
   return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
 }
 
-// chunk swizzle for a K tile row of HD halfs (HD/8 chunks of 16 bytes): eight consecutive rows
-// read at one logical chunk land in eight different 16-byte bank groups (HD >= 64), or the four
-// chunks of a 64-byte row pair up with the row parity bits (HD = 32).
+// Chunk swizzles of the LDS tiles.  One ds_read_b128 phase serves 16 lanes, which read 16
+// consecutive rows at one logical 16-byte chunk; the physical chunk is XORed with row bits chosen so
+// that those 16 rows land in 16 different 16-byte bank groups (64 banks x 4 bytes = 256 bytes):
+// 64-byte rows (HD 32) pair the 4 chunks with bits 2-3 of the row, 128-byte rows (HD 64, and the
+// 64-key V^T rows) the 8 chunks with bits 1-3, 256- and 512-byte rows (HD 128, 256) 16 chunks with
+// bits 0-3.  The global -> LDS copies fetch logical chunk c ^ swizzle into physical chunk c, so any
+// per-row XOR works with them.
 template <int HD>
 __device__ __forceinline__ int kswz(int row, int c) {
-  if constexpr (HD >= 64) return c ^ (row & 7);
-  else return c ^ ((row >> 1) & 3);
+  if constexpr (HD >= 128) return c ^ (row & 15);
+  else if constexpr (HD == 64) return c ^ ((row >> 1) & 7);
+  else return c ^ ((row >> 2) & 3);
 }
+__device__ __forceinline__ int vswz(int row, int c) { return c ^ ((row >> 1) & 7); }
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
@@ -128,7 +134,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
 #pragma unroll
   for (int c = 0; c < VCOPIES; ++c) {
     const int d = (wave * VCOPIES + c) * 8 + (lane >> 3);
-    voff[c] = d * ldv + ((lane & 7) ^ (d & 7)) * 8;
+    voff[c] = d * ldv + vswz(d, lane & 7) * 8;
   }
   auto issue_tile = [&](int t0, int st) {
 #pragma unroll
@@ -146,7 +152,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     const int first = S - t0;  // first invalid column of this tile, in (0, 64)
     for (int e = tid; e < HD * kBKV; e += 256) {
       const int d = e / kBKV, k = e % kBKV;
-      if (k >= first) sv[st][d * kBKV + swz(d, k / 8) * 8 + (k & 7)] = (half)0.f;
+      if (k >= first) sv[st][d * kBKV + vswz(d, k / 8) * 8 + (k & 7)] = (half)0.f;
     }
   };
 
@@ -269,7 +275,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
-            const half8 a = *(const half8*)(&sv[st][row * kBKV + swz(row, 4 * kb + 2 * c + hf) * 8]);
+            const half8 a = *(const half8*)(&sv[st][row * kBKV + vswz(row, 4 * kb + 2 * c + hf) * 8]);
             o[i] = mfma32x32x16(a, p16[kb][c], o[i]);
           }
       }

@@ -142,9 +142,4 @@ __device__ __forceinline__ float gelu_erf(float v) {
   return fmaf(-a, q, fmaxf(v, 0.f));
 }
 
-// 16-byte element chunk index swizzle for [rows][64 halfs] LDS tiles (128-byte rows): XOR with the
-// row's low three bits so that the eight lanes of one ds_read_b128 phase, which read eight
-// consecutive rows at the same logical chunk, hit eight different 16-byte bank groups.
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (row & 7); }
-
 }  // namespace tt

@@ -4,7 +4,7 @@
 // Design (gfx950):
 //  * Both operands are K-contiguous (nn.Linear weights are [N,K]), so a block stages a BM x 64
 //    X tile and a BN x 64 W tile in LDS per K step (128-byte rows, 16-byte chunks XOR-swizzled
-//    by row so ds_read_b128 fragment reads are bank-conflict free), double-buffered.  The copies
+//    by row bits 1-3 so ds_read_b128 fragment reads are bank-conflict free), double-buffered.  The copies
 //    are global_load_lds_dwordx4 (global -> LDS without a register round trip), issued for the
 //    next K step during the first half of the current one, one between consecutive MFMAs, with
 //    the next k-step's fragment reads interleaved the same way (sched_group_barrier).
@@ -129,8 +129,8 @@ __device__ void fill_padded_tile(const EpiArgs& ep, int M, int m0, int n0) {
 // LDS tile of R rows x 64 halfs (128-byte rows) holding a K slice of one operand.  Global ->
 // LDS copies use global_load_lds_dwordx4: one instruction moves 1 KiB, lane l writing LDS bytes
 // [16 l, 16 l + 16) of an 8-row group, i.e. row l / 8, physical chunk l % 8.  The chunk swizzle is
-// applied on the global side: lane l fetches logical chunk (l % 8) ^ (l / 8) of its row, so the
-// physical chunk of logical chunk c in row r is c ^ (r % 8), as swz() expects.
+// applied on the global side: lane l fetches logical chunk (l % 8) ^ ((r >> 1) % 8) of its row r,
+// so the physical chunk of logical chunk c in row r is c ^ ((r >> 1) % 8).
 
 // Register-path staging (PATH = 1): each thread moves 16-byte chunks global -> VGPR -> LDS with
 // buffer loads and ds_write_b128, two K stages ahead in two register sets, so a CU keeps three K
@@ -199,8 +199,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
     *(u32x4*)(sbias + 8 * threadIdx.x) = *(const u32x4*)(ep.bias + n0 + 8 * threadIdx.x);
 
   // Fragment addressing: A = W rows (output features), B = X rows (tokens); lane l reads row
-  // l % 32 of a 32-row block at logical chunk 2 kk + l / 32, physically XOR (l % 8).
-  const int frow = lane & 31, fhi = lane >> 5, fx = lane & 7;
+  // l % 32 of a 32-row block at logical chunk 2 kk + l / 32, physically XOR bits 1-3 of the row
+  // (the direct-copy layout below).
+  const int frow = lane & 31, fhi = lane >> 5, fx = (lane >> 1) & 7;
   half8 af[2][FN], bf[2][FM];
   auto frags = [&](int buf, int kk, const half* stage) {
     const int pc = PATH ? 2 * kk + fhi : (2 * kk + fhi) ^ fx;
@@ -217,7 +218,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
     // are clamped to M - 1 (valid memory whose results are never stored).
     // Offsets are relative to the block's first X row and W row (64-bit bases), so M * K may
     // exceed 2^31 (long sequences); BM * K and BN * K stay far below it.
-    const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
+    // Chunk layout: physical chunk = logical ^ bits 1-3 of the row, so that the 16 consecutive rows
+    // one ds_read_b128 phase reads land in 16 different bank groups (with bits 0-2, rows r and
+    // r + 8 would share banks).  Row (wave + 4 i) * 8 + lrow has bits 1-3 = (wave & 1) << 2 |
+    // lrow >> 1 for every i.
+    const int lrow = lane >> 3, lchunk = (lane & 7) ^ (((wave & 1) << 2) | (lrow >> 1));
     const half* Xb = X + (size_t)m0 * K;
     const half* Wb = W + (size_t)n0 * K;
     int src_off[NL];
