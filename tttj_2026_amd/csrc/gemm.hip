@@ -4,8 +4,9 @@
 // Design (gfx950):
 //  * Both operands are K-contiguous (nn.Linear weights are [N,K]), so a block stages a BM x 64
 //    X tile and a BN x 64 W tile in LDS per K step (128-byte rows, 16-byte chunks XOR-swizzled
-//    by row bits 1-3 so ds_read_b128 fragment reads are bank-conflict free), double-buffered.  The copies
-//    are global_load_lds_dwordx4 (global -> LDS without a register round trip), issued for the
+//    by row bits 1-3 so ds_read_b128 fragment reads are bank-conflict free), double-buffered.
+//    The copies are global_load_lds_dwordx4 (global -> LDS without a register round trip), or
+//    buffer loads through VGPRs into padded rows on the register path; issued for the
 //    next K step during the first half of the current one, one between consecutive MFMAs, with
 //    the next k-step's fragment reads interleaved the same way (sched_group_barrier).
 //  * The MFMA is v_mfma_f32_32x32x16_f16 with W as the "A" operand and X as "B", i.e. each wave
@@ -153,8 +154,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
   constexpr int ROWS = BM + BN;       // LDS rows per stage: X rows [0, BM), W rows [BM, BM + BN)
   // LDS row stride in halfs: 128-byte rows with XOR-swizzled chunks for the direct copies (one
   // copy instruction fills 1 KiB contiguously, so rows cannot be padded); rows padded to 144 bytes
-  // on the register path, which leaves the 16 rows one ds_read_b128 phase reads in 16 different
-  // bank groups (the XOR swizzle covers only 8: rows r and r + 8 share banks).
+  // and unswizzled on the register path.  Either way the 16 rows one ds_read_b128 phase reads fall
+  // in 16 different bank groups.
   constexpr int LDR = PATH ? kBK + 8 : kBK;
   constexpr int STAGE = ROWS * LDR;   // halfs per stage
   constexpr int XL = BM / 32;         // X copies per wave per stage (8 rows x 4 waves each)
