@@ -165,7 +165,8 @@ def test_linear_masked_rows(device, m, n, k, seq, mode, tile):
 @pytest.mark.parametrize("tile", [-1, 0, 2, 4, 5, 6, 7, 8, 9])
 @pytest.mark.parametrize("b,s,d,h", [(4, 256, 512, 8), (3, 100, 256, 4), (2, 1024, 1024, 16),
                                      (4, 100, 32, 4), (2, 130, 96, 3), (3, 128, 128, 16),
-                                     (2, 64, 1024, 4), (2, 72, 128, 1)])
+                                     (2, 64, 1024, 4), (2, 72, 128, 1), (5, 3, 64, 2),
+                                     (6, 12, 128, 4), (3, 40, 256, 2)])
 def test_qkv_projection_masked_tokens(device, b, s, d, h, tile):
     """Masked tokens get +0.0 in Q, K and V^T (whole masked tiles skip the MMA); others match."""
     lib = _lib.load()
@@ -239,7 +240,8 @@ def test_linear_small_shapes(device, m, n, k, mode, masked):
 
 
 # ---------------------------------------------------------------- QKV layout + attention
-@pytest.mark.parametrize("b,s,d,h", [(2, 64, 256, 8), (1, 100, 128, 2), (3, 128, 512, 8)])
+@pytest.mark.parametrize("b,s,d,h", [(2, 64, 256, 8), (1, 100, 128, 2), (3, 128, 512, 8),
+                                     (11, 6, 64, 1), (9, 24, 512, 4), (4, 200, 256, 2)])
 def test_qkv_projection_layout(device, b, s, d, h):
     x = _rand((b, s, d), 40)
     w = _rand((3 * d, d), 41, 1.0 / math.sqrt(d))
@@ -322,14 +324,34 @@ def test_attention_benchmark_shapes(device, b, s, h, hd, causal):
     k = _rand((b, h, s, hd), 61, 1.0)
     vt = _rand((b, h, hd, (s + 63) // 64 * 64), 62, 1.0)
     mask = _masks("prefix", b, s, 63) if b == 8 else None
-    ctx = ops.attention(q, k, vt, None if mask is None else mask.to(device), causal)
+    # NaN-filled output: every (sequence, head, query tile) block must write its rows, so a block
+    # order that skips or repeats a tile leaves NaN behind.
+    ctx = torch.full((b, s, h * hd), float("nan"), dtype=torch.float16, device=device)
+    ops.attention(q, k, vt, None if mask is None else mask.to(device), causal, out=ctx)
     torch.cuda.synchronize()
-    # spot-check two heads' worth of rows against the fp32 reference (full reference is large)
+    assert torch.isfinite(ctx).all().item()
+    # full fp32 reference for the first sequence (the full reference is large) ...
     sl = slice(0, 1)
     ref = _attention_ref(q[sl], k[sl], vt[sl], None if mask is None else mask[sl], causal)
     got = ctx[sl].float().cpu()
     if mask is not None:
         got, ref = got[mask[sl]], ref[mask[sl]]
+    assert (got - ref).abs().max().item() <= 6e-3
+    # ... and, for every sequence and head, the first and last row of every query tile
+    rows = sorted({r for t in range(0, s, 128) for r in (t, min(t + 127, s - 1))})
+    qf, kf = q.float().cpu(), k.float().cpu()
+    vf = vt[..., :s].float().cpu()
+    sc = torch.matmul(qf[:, :, rows], kf.transpose(-1, -2).contiguous()) / math.sqrt(hd)
+    allowed = torch.ones(b, 1, len(rows), s, dtype=torch.bool)
+    if causal:
+        allowed &= torch.arange(s)[None, :] <= torch.tensor(rows)[:, None]
+    if mask is not None:
+        allowed &= mask[:, None, None, :]
+    p = torch.softmax(sc.masked_fill(~allowed, float("-inf")), dim=-1).nan_to_num(0.0)
+    ref = torch.matmul(p, vf.transpose(-1, -2).contiguous()).permute(0, 2, 1, 3).reshape(b, len(rows), h * hd)
+    got = ctx[:, rows].float().cpu()
+    if mask is not None:
+        ref = ref * mask[:, rows, None]  # padded query rows are written as zeros
     assert (got - ref).abs().max().item() <= 6e-3
 
 

@@ -440,20 +440,29 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
   if (vt_mode) {
     // V^T rows: staged row nl holds WM consecutive tokens of feature nw + nl.  S % 8 == 0 here,
     // so an aligned group of 8 tokens lies in one sequence and M is a multiple of 8.
+    // The lane's 8 tokens (m .. m + 7) are fixed, so their (sequence, position) is one division;
+    // the feature row advances by RPI per iteration and its (head, feature) pair is stepped
+    // instead of divided (integer division is a ~20-instruction VALU sequence).
     constexpr int CPR = WM / 8, RPI = 64 / CPR;
     const int D = ep.d_model, hd = ep.head_dim, S = ep.seq;
     const size_t plane = (size_t)ep.batch * S * D;
     const size_t ldv = (size_t)(S + 63) / 64 * 64;
+    const int c = lane % CPR, m = mw + 8 * c;
+    if (m >= M) return;
+    const int bb = m / S, sq = m - bb * S;
+    half* vbase = ep.y + 2 * plane + (size_t)bb * ep.heads * hd * ldv + sq;
+    const int nn0 = nw + lane / CPR - 2 * D;
+    int hh = nn0 / hd, d = nn0 - hh * hd;
 #pragma unroll 4
     for (int it = 0; it < WN / RPI; ++it) {
-      const int r = it * RPI + lane / CPR, c = lane % CPR;
-      const int m = mw + 8 * c;
-      if (m >= M) continue;
+      const int r = it * RPI + lane / CPR;
       const half8 t = *(const half8*)(cst + r * WM + 8 * c);
-      const int nn = nw + r - 2 * D;
-      const int hh = nn / hd, d = nn - hh * hd;
-      const int bb = m / S, sq = m - bb * S;
-      *(half8*)(ep.y + 2 * plane + (((size_t)bb * ep.heads + hh) * hd + d) * ldv + sq) = t;
+      *(half8*)(vbase + ((size_t)hh * hd + d) * ldv) = t;
+      d += RPI;
+      while (d >= hd) {  // at most RPI / hd + 1 steps
+        d -= hd;
+        ++hh;
+      }
     }
     return;
   }
@@ -464,6 +473,23 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
   constexpr int NB = NIT < 8 ? NIT : 8;
   constexpr bool RESID = MODE == TT_EPI_RESID_MASKED || MODE == TT_EPI_MASKED_RESID;
   const int c = lane % CPR;
+  // Q / K destinations, [B, H, S, hd]: the lane's 8 features (one head) are fixed, so the column
+  // part is one base pointer; the row m = mw + r advances by RPI per store and its (sequence,
+  // position) pair is stepped (one wrap per store once S >= RPI) instead of divided.
+  [[maybe_unused]] half* qk_col = nullptr;
+  [[maybe_unused]] int qk_sq = 0;
+  [[maybe_unused]] size_t qk_row = 0;  // ((b H) S + sq) hd for the current row
+  if constexpr (MODE == TT_EPI_QKV) {
+    const int D = ep.d_model, hd = ep.head_dim, S = ep.seq;
+    const int n = nw + 8 * c;
+    const int which = n / D, nn = n - which * D;
+    const int hh = nn / hd, d = nn - hh * hd;
+    qk_col = ep.y + which * ((size_t)ep.batch * S * D) + (size_t)hh * S * hd + d;
+    const int m = mw + lane / CPR;
+    const int bb = m / S;
+    qk_sq = m - bb * S;
+    qk_row = ((size_t)bb * ep.heads * S + qk_sq) * hd;
+  }
 #pragma unroll
   for (int b0 = 0; b0 < NIT; b0 += NB) {
     half8 rv[NB];
@@ -483,6 +509,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
       const int sw = r & SWM;
       half8 t = *(const half8*)(cst + r * WN + (((2 * c) ^ (sw & ~1)) << 2));
       if (sw & 1) t = swap_halves(t);
+      [[maybe_unused]] size_t row_off = 0;
+      if constexpr (MODE == TT_EPI_QKV) {
+        row_off = qk_row;
+        const int S = ep.seq, hd = ep.head_dim;
+        qk_sq += RPI;
+        qk_row += (size_t)RPI * hd;
+        while (qk_sq >= S) {  // next row crosses into the next sequence
+          qk_sq -= S;
+          qk_row += (size_t)(ep.heads - 1) * S * hd;
+        }
+      }
       if (m >= M) continue;
       if constexpr (RESID) {
 #pragma unroll
@@ -495,14 +532,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
       }
       half* dst;
       if constexpr (MODE == TT_EPI_QKV) {
-        // Q or K: 8 features of one head of token m -> [B, H, S, hd] row
-        const int D = ep.d_model, hd = ep.head_dim, S = ep.seq;
-        const int n = nw + 8 * c;
-        const int which = n / D, nn = n - which * D;
-        const int hh = nn / hd, d = nn - hh * hd;
-        const int bb = m / S, sq = m - bb * S;
-        dst = ep.y + which * ((size_t)ep.batch * S * D) +
-              (((size_t)bb * ep.heads + hh) * S + sq) * hd + d;
+        dst = qk_col + row_off;  // Q or K: 8 features of one head of token m
       } else {
         dst = ep.y + (size_t)m * ep.ldy + nw + 8 * c;
       }

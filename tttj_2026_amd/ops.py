@@ -110,8 +110,11 @@ def mask_info(mask: Optional[torch.Tensor], batch: int, seq: int, device) -> tor
 
 
 def attention(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, mask: Optional[torch.Tensor],
-              causal: bool) -> torch.Tensor:
-    """q, k [B,H,S,hd], vt [B,H,hd,Sp] (views from qkv_projection) -> ctx [B,S,H*hd]."""
+              causal: bool, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """q, k [B,H,S,hd], vt [B,H,hd,Sp] (views from qkv_projection) -> ctx [B,S,H*hd].
+
+    `out`, if given, is a contiguous fp16 [B,S,H*hd] tensor on the same device that receives ctx.
+    """
     b, h, s, hd = q.shape
     if k.shape != q.shape or vt.shape[:3] != (b, h, hd) or vt.shape[3] != (s + 63) // 64 * 64:
         raise ValueError("inconsistent q/k/vt shapes")
@@ -120,7 +123,13 @@ def attention(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, mask: Optional
             raise ValueError(f"{name} must be contiguous fp16")
     mask = _mask(mask, b * s)
     info = mask_info(mask, b, s, q.device) if mask is not None else None
-    ctx = torch.empty(b, s, h * hd, dtype=torch.float16, device=q.device)
+    if out is None:
+        ctx = torch.empty(b, s, h * hd, dtype=torch.float16, device=q.device)
+    elif (out.shape != (b, s, h * hd) or out.dtype != torch.float16 or not out.is_contiguous()
+          or out.device != q.device):
+        raise ValueError("out must be a contiguous fp16 [B,S,H*hd] tensor on q's device")
+    else:
+        ctx = out
     rc = _lib.load().tt_attention_fwd(q.data_ptr(), k.data_ptr(), vt.data_ptr(), _ptr(mask),
                                       _ptr(info), ctx.data_ptr(), b, s, h, hd, int(causal),
                                       _stream(q))
