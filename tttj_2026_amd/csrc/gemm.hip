@@ -233,9 +233,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
       if (i < XL) src_off[i] = min(r, M - 1 - m0) * K + lchunk * 8;
       else src_off[i] = (r - BM) * K + lchunk * 8;
     }
+    // The wave index is made provably uniform so the LDS destination (M0) is scalar arithmetic;
+    // the source is a uniform base advanced by k0 plus the lane's fixed 32-bit offset, which
+    // lets the copy use the scalar-base addressing mode (no per-copy 64-bit VALU adds).
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     auto copy = [&](int i, int k0, half* stage) {
-      const half* base = (i < XL) ? Xb : Wb;
-      lds_copy16(base + src_off[i] + k0, stage + (wave + 4 * i) * 8 * kBK);
+      const half* base = ((i < XL) ? Xb : Wb) + k0;
+      lds_copy16(base + (uint32_t)src_off[i], stage + (wave_u + 4 * i) * 8 * kBK);
     };
 
     // One stage: KSUB k-steps of FN x FM MFMAs.  Fragment reads for k-step kk + 1 and (MORE) the
@@ -285,13 +289,26 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
     for (int i = 0; i < NL; ++i) copy(i, 0, lds);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    for (int kt = 0; kt < nk - 1; ++kt) {
-      stage(std::true_type{}, lds + (kt & 1) * STAGE, lds + ((kt + 1) & 1) * STAGE, (kt + 1) * kBK);
-      // The next stage's copies have landed in LDS and every wave is done reading this stage.
+    // Unrolled by two so that both stage buffers are constant offsets (fragment reads then use
+    // immediate offsets instead of one address add each).  After each stage: the next stage's
+    // copies have landed in LDS and every wave is done reading this one.
+    int kt = 0;
+    for (; kt + 2 < nk; kt += 2) {
+      stage(std::true_type{}, lds, lds + STAGE, (kt + 1) * kBK);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      stage(std::true_type{}, lds + STAGE, lds, (kt + 2) * kBK);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
     }
-    stage(std::false_type{}, lds + ((nk - 1) & 1) * STAGE, nullptr, 0);
+    if (kt + 1 < nk) {  // two stages left (kt is even: stage kt is in the first buffer)
+      stage(std::true_type{}, lds, lds + STAGE, (kt + 1) * kBK);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      stage(std::false_type{}, lds + STAGE, nullptr, 0);
+    } else {
+      stage(std::false_type{}, lds, nullptr, 0);
+    }
 
   } else {
     // Register path.  Thread t moves chunk t % 8 of rows t / 8 + 32 i (i < RX: X rows, then W
