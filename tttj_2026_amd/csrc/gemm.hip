@@ -805,12 +805,13 @@ static int pick_tile(int m, int n, int k, int mode, int cus) {
     return g_tile_override;
   auto tiles = [&](int i) { return (long)((m + kTiles[i].bm - 1) / kTiles[i].bm) * (n / kTiles[i].bn); };
   if (k >= 4096 && n % 256 == 0 && tiles(0) >= cus) return 0;
-  // Register-path tiles with padded LDS rows, where they measured ahead of the direct copies
-  // (MI355X, M = 8192, medians of interleaved runs): 256 x 128 for one round of tiles with
-  // K >= 4096 (N = 1024: 77.5 -> 75.1 us) and 128 x 128 for the GELU epilogue (N = 4096, K = 1024:
-  // 101.5 -> 96.7 us; two blocks per CU overlap one block's GELU with the other's MFMAs).  For
-  // the other M = 8192 projections the two paths tie.
-  if (k >= 4096 && n % 128 == 0 && tiles(9) >= cus) return 9;
+  // Register-path 128 x 128 tiles with padded LDS rows for the GELU epilogue, where they measured
+  // ahead of the direct copies (MI355X, M = 8192, N = 4096, K = 1024, medians of interleaved runs:
+  // 101.5 -> 96.7 us; two blocks per CU overlap one block's GELU with the other's MFMAs).  For the
+  // other M = 8192 projections the direct 128 x 128 tiles are as fast or faster (ffn_out,
+  // N = 1024, K = 4096, alone: 69.4 us against 73.2 for register-path 256 x 128 tiles and 73.0 for
+  // direct 256 x 128 ones; in whole forwards C5 is unchanged and C4 gains 0.8%, its padded rows
+  // filling more whole 128-row tiles than 256-row ones).
   if (mode == TT_EPI_BIAS_GELU && n % 128 == 0 && tiles(7) >= cus) return 7;
   // One round of 128 x 64 tiles streaming a long K is latency-bound: each CU moves only the bytes
   // it keeps in flight, and the register path keeps two more K stages in flight than the direct
