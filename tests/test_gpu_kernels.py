@@ -26,7 +26,8 @@ def _bits_zero(t):
 
 
 # ---------------------------------------------------------------- LayerNorm
-@pytest.mark.parametrize("rows,d", [(1, 256), (3, 512), (1000, 1024), (77, 96), (5, 8192), (4096, 256)])
+@pytest.mark.parametrize("rows,d", [(1, 256), (3, 512), (1000, 1024), (77, 96), (5, 8192), (4096, 256),
+                                    (8192, 1024), (20001, 512), (6000, 2048)])
 def test_layernorm(device, rows, d):
     x = _rand((rows, d), 1, scale=3.0) + 0.5
     w = _rand((d,), 2, scale=0.3) + 1.0
