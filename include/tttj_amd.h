@@ -98,6 +98,31 @@ int tt_resolve_plan(int batch, int seq, int d_model, int num_heads, int ffn_dim,
 int tt_megakernel_status(const void* workspace, int batch, int seq, int d_model, int ffn_dim,
                          int num_layers, int* status, void* stream);
 
+/* Byte offset, inside a megakernel workspace for this shape, of its 32-bit error word: 0 while
+ * every dependency wait completed, non-zero once one gave up (then that launch wrote NaN over all
+ * of y, and so does every later launch until the workspace is zero-filled again).  Lets a caller
+ * copy the word asynchronously and check it later, without the stream synchronisation of
+ * tt_megakernel_status.  No counterpart in the reference (its waits are unbounded,
+ * kernels/dag_megakernel.py:1355-1367). */
+int tt_megakernel_error_offset(int batch, int seq, int d_model, int num_heads, int ffn_dim,
+                               int num_layers, int64_t* offset);
+
+/* Attach a host word to a megakernel workspace (after it is zero-filled; zero-filling detaches
+ * it): at the end of every later launch on that workspace the last workgroup writes the error
+ * flag (0 or 1) to *host_status, so a caller can check a launch's health by reading host memory,
+ * without a stream synchronisation or an extra copy.  host_status must be device-accessible
+ * pinned host memory (hipHostMalloc) that outlives the workspace's use, or NULL to detach.  The
+ * attachment itself is a stream-ordered kernel on `stream`.  No counterpart in the reference. */
+int tt_megakernel_attach_status(void* workspace, int64_t workspace_bytes, int batch, int seq,
+                                int d_model, int num_heads, int ffn_dim, int num_layers,
+                                int32_t* host_status, void* stream);
+
+/* Test hook: polls per megakernel dependency wait (each poll followed by a one-step s_sleep)
+ * before the wait gives up, for every later launch; limit < 0 restores the default (2^22).  A
+ * small limit makes waits give up early while every wave still exits, which lets tests exercise
+ * the error path.  Process wide, not thread-safe.  No counterpart in the reference. */
+int tt_megakernel_set_spin_limit(int64_t limit);
+
 /* Number of DAG tasks of the megakernel plan for this shape (<0 on bad arguments). */
 int tt_megakernel_tasks(int batch, int seq, int d_model, int num_heads, int ffn_dim,
                         int num_layers);

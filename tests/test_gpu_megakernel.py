@@ -98,3 +98,40 @@ def test_megakernel_workspace_survives_shape_changes(device):
         res = O.check_tolerance(y, O.forward(p32, x16.float(), mask, 4, True), mask)
         assert res["passed"], (b, s, res)
         assert mk.megakernel_status(b, s) == 0
+
+
+def test_megakernel_wait_expiry_raises_and_recovers(device):
+    """A dependency wait that gives up must not turn into silent garbage.  With the spin limit
+    forced to 0 from the host (the kernel's own bounded wait gives up at its first unready poll,
+    every later wait falls through, every wave exits), the launch writes NaN over its output; the
+    next forward raises MegakernelWaitError and re-arms the workspace; the one after is correct."""
+    from tttj_2026_amd import _lib
+    from tttj_2026_amd.optimized_transformer import MegakernelWaitError
+
+    cfg = TransformerConfig(1, 64, 256, 8, 1024, 4, True)   # C2 shape
+    gm = build_model(cfg, seed=5).half().to(device).eval()
+    mk = make_optimized_transformer(copy.deepcopy(gm), plan=PLAN_MEGAKERNEL)
+    x16, _ = make_inputs(cfg, False, 6)
+    xd = x16.to(device)
+    lib = _lib.load()
+    print("[megakernel] spin limit 0", flush=True)
+    assert lib.tt_megakernel_set_spin_limit(0) == 0
+    try:
+        with torch.inference_mode():
+            y_bad = mk(xd, None)
+        torch.cuda.synchronize()
+    finally:
+        lib.tt_megakernel_set_spin_limit(-1)
+    assert mk.megakernel_status(1, 64) == 1
+    assert torch.isnan(y_bad).all()
+    with pytest.raises(MegakernelWaitError):
+        with torch.inference_mode():
+            mk(xd, None)
+    assert mk.megakernel_status(1, 64) == 0
+    with torch.inference_mode():
+        y = mk(xd, None)
+    torch.cuda.synchronize()
+    assert mk.megakernel_status(1, 64) == 0
+    ref = O.forward(O.params_fp32(gm), x16.float(), None, 8, True)
+    res = O.check_tolerance(y, ref, None)
+    assert res["passed"], res

@@ -176,3 +176,50 @@ def test_case_number_for_model_mirrors_reference():
         cfg = reference_case_config(1)
         case_number_for_model(Holder(TransformerConfig(cfg.batch_size, cfg.seq_len, cfg.d_model,
                                                        cfg.num_heads, cfg.ffn_dim, 3, True)))
+
+
+def test_megakernel_health_check_raises_and_rearms(monkeypatch):
+    """Host logic of the megakernel health word, with a stubbed status (no GPU): a non-zero word
+    raises MegakernelWaitError after zero-filling the workspace, clearing the word and
+    re-attaching it; a zero word does nothing."""
+    from tttj_2026_amd import optimized_transformer as OT
+
+    class _Stream:
+        def synchronize(self):
+            pass
+
+    monkeypatch.setattr(OT.torch.cuda, "current_stream", lambda *a, **k: _Stream())
+    cfg = TransformerConfig(1, 64, 256, 8, 1024, 4, True)
+    mod = OT.OptimizedTransformer(build_model(cfg), plan=OT.PLAN_MEGAKERNEL)
+    attached = []
+    monkeypatch.setattr(mod, "_attach", lambda entry, b, s: attached.append((b, s)))
+    ws = torch.full((64,), 7, dtype=torch.uint8)
+    status = torch.zeros(1, dtype=torch.int32)
+    entry = (ws, status, status.numpy())
+    mod._check_mega_health(entry, 1, 64)            # healthy: nothing happens
+    assert attached == [] and (ws == 7).all()
+    status[0] = 1                                   # the kernel reported an expired wait
+    with pytest.raises(OT.MegakernelWaitError):
+        mod._check_mega_health(entry, 1, 64)
+    assert (ws == 0).all() and int(status[0]) == 0 and attached == [(1, 64)]
+    mod._check_mega_health(entry, 1, 64)            # re-armed
+    assert attached == [(1, 64)]
+
+
+def test_megakernel_workspaces_are_bounded(monkeypatch):
+    """At most MEGA_WORKSPACES_KEPT megakernel workspaces are kept, least recently used dropped
+    first; a shape used again keeps its workspace (and so its counters and epoch)."""
+    from tttj_2026_amd import optimized_transformer as OT
+
+    cfg = TransformerConfig(1, 64, 256, 8, 1024, 4, True)
+    mod = OT.OptimizedTransformer(build_model(cfg), plan=OT.PLAN_MEGAKERNEL)
+    monkeypatch.setattr(mod, "_attach", lambda entry, b, s: None)
+    monkeypatch.setattr(mod, "_new_status_word", lambda: torch.zeros(1, dtype=torch.int32))
+    cpu = torch.device("cpu")
+    first = mod._mega_entry(1, 64, 0, 16, cpu)[0]
+    for s in (65, 66, 67):
+        mod._mega_entry(1, s, 0, 16, cpu)
+    assert mod._mega_entry(1, 64, 0, 16, cpu)[0] is first     # reused, now most recent
+    mod._mega_entry(1, 68, 0, 16, cpu)                          # evicts (1, 65)
+    assert list(mod._mega) == [(1, 66, 0), (1, 67, 0), (1, 64, 0), (1, 68, 0)]
+    assert len(mod._mega) == OT.MEGA_WORKSPACES_KEPT

@@ -72,17 +72,54 @@ def test_golden_generate_random_case_matches_reference(golden):
         np.testing.assert_array_equal(mask.numpy(), golden[f"{case}/mask"])
 
 
+def _golden_forward_params(golden, case):
+    """The weights the reference forward ran with: the LayerNorm-perturbed set where the case
+    has one, else the seeded default init."""
+    pre = f"{case}/fwd_param/" if any(k.startswith(f"{case}/fwd_param/") for k in golden.files) \
+        else f"{case}/param/"
+    return {k[len(pre):]: torch.from_numpy(golden[k]) for k in golden.files if k.startswith(pre)}
+
+
+def _golden_forward_inputs(golden, case):
+    """(x, mask) the reference forward ran on: the case's own mask where it has one, else the
+    generator's draw."""
+    xk, mk = (f"{case}/fwd_x", f"{case}/fwd_mask") if f"{case}/fwd_x" in golden.files \
+        else (f"{case}/x", f"{case}/mask")
+    return torch.from_numpy(golden[xk]), torch.from_numpy(golden[mk])
+
+
 def test_golden_forward_oracle_vs_bruteforce(golden):
     """The fixture inputs through both restatements (weights are the reference's own)."""
     for case in _golden_cases(golden):
         b, s, d, h, f, layers, causal, seed = (int(v) for v in golden[f"{case}/meta"])
-        p = {k[len(case) + 7:]: torch.from_numpy(golden[k]) for k in golden.files
-             if k.startswith(f"{case}/param/")}
-        x = torch.from_numpy(golden[f"{case}/x"])
-        mask = torch.from_numpy(golden[f"{case}/mask"])
+        p = _golden_forward_params(golden, case)
+        x, mask = _golden_forward_inputs(golden, case)
         out = O.forward(p, x, mask, h, bool(causal)).double().numpy()
         bf = O.bruteforce_forward(p, x, mask, h, bool(causal))
         np.testing.assert_allclose(out, bf, atol=2e-5, rtol=0)
+
+
+def test_golden_forward_matches_reference_output(golden):
+    """Both restatements against the reference BaselineTransformer's own forward output
+    (float64 module copy and float32), on causal and non-causal cases, prefix and non-prefix
+    masks, a fully padded sequence and perturbed LayerNorm parameters."""
+    cases = _golden_cases(golden)
+    assert {"masked_noncausal_ln", "nonprefix_causal_ln"} <= set(cases)
+    for case in cases:
+        b, s, d, h, f, layers, causal, seed = (int(v) for v in golden[f"{case}/meta"])
+        p = _golden_forward_params(golden, case)
+        x, mask = _golden_forward_inputs(golden, case)
+        y64 = golden[f"{case}/y_fp64"]
+        y32 = golden[f"{case}/y_fp32"]
+        out = O.forward(p, x, mask, h, bool(causal))
+        np.testing.assert_allclose(out.double().numpy(), y64, atol=1e-5, rtol=0, err_msg=case)
+        np.testing.assert_allclose(out.numpy(), y32, atol=1e-5, rtol=0, err_msg=case)
+        # the reference rounds its softmax to fp32 even in a float64 module (scores.float(),
+        # torch_transformer_benchmark.py:111), so the float64 brute force differs by ~1e-7
+        bf = O.bruteforce_forward(p, x, mask, h, bool(causal))
+        np.testing.assert_allclose(bf, y64, atol=1e-6, rtol=0, err_msg=case)
+        # padded rows are exactly zero in the reference output and in the oracle's
+        assert (y64[~mask.numpy()] == 0).all() and (out[~mask] == 0).all()
 
 
 # ---------------------------------------------------------------- brute force

@@ -33,6 +33,9 @@ SIGNATURES = {
     "tt_resolve_plan": (_I, [_I, _I, _I, _I, _I, _I]),
     "tt_megakernel_status": (_I, [_P, _I, _I, _I, _I, _I, ctypes.POINTER(_I), _P]),
     "tt_megakernel_tasks": (_I, [_I, _I, _I, _I, _I, _I]),
+    "tt_megakernel_error_offset": (_I, [_I, _I, _I, _I, _I, _I, ctypes.POINTER(_I64)]),
+    "tt_megakernel_set_spin_limit": (_I, [_I64]),
+    "tt_megakernel_attach_status": (_I, [_P, _I64, _I, _I, _I, _I, _I, _I, _P, _P]),
     "tt_megakernel_trace_fwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _I, _I, _P,
                                      _I64, _P]),
     "tt_layernorm_fwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _P]),
@@ -98,6 +101,14 @@ def workspace_bytes(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int
     out = _I64()
     check(load().tt_workspace_bytes(batch, seq, d_model, heads, ffn_dim, num_layers, plan,
                                     ctypes.byref(out)), "tt_workspace_bytes")
+    return out.value
+
+
+def megakernel_error_offset(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,
+                            num_layers: int) -> int:
+    out = _I64()
+    check(load().tt_megakernel_error_offset(batch, seq, d_model, heads, ffn_dim, num_layers,
+                                            ctypes.byref(out)), "tt_megakernel_error_offset")
     return out.value
 
 

@@ -13,6 +13,7 @@
 
 #include <cstdarg>
 #include <cstring>
+#include <mutex>
 
 namespace tt {
 
@@ -202,10 +203,14 @@ extern "C" int tt_megakernel_status(const void* workspace, int batch, int seq, i
                            (hipStream_t)stream);
 }
 
-extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint8_t* mask, void* y,
-                                  void* workspace, int64_t workspace_bytes, int batch, int seq,
-                                  int d_model, int num_heads, int ffn_dim, int num_layers,
-                                  int causal, int plan, void* stream_) {
+namespace tt {
+
+// The forward on a workspace the caller provides (tt_transformer_fwd) or on the library's own
+// scratch array (tt_transformer_fwd_noalloc, which clears the megakernel's counters first).
+int transformer_fwd(const void* weights, const void* x, const uint8_t* mask, void* y,
+                           void* workspace, int64_t workspace_bytes, int batch, int seq,
+                           int d_model, int num_heads, int ffn_dim, int num_layers, int causal,
+                           int plan, bool reset_counters, void* stream_) {
   int rc = check_model_shape(batch, seq, d_model, num_heads, ffn_dim, num_layers);
   if (rc != TT_OK) return rc;
   TT_REQUIRE(weights && x && y && workspace, "transformer: null pointer");
@@ -215,6 +220,10 @@ extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint
   const int T = B * S, hd = D / H;
   if (resolve_plan(plan, B, S, D, H, F) == TT_PLAN_MEGAKERNEL) {
     const Layout lay = weight_layout(D, F, L);
+    if (reset_counters &&
+        (rc = megakernel_reset(workspace, workspace_bytes, B, S, D, H, F, L,
+                               (hipStream_t)stream_)) != TT_OK)
+      return rc;
     return launch_megakernel((const half*)weights, lay.off, lay.stride, lay.final_off,
                              (const half*)x, mask, (half*)y, (char*)workspace, workspace_bytes, B,
                              S, D, H, F, L, causal, nullptr, (hipStream_t)stream_);
@@ -308,4 +317,39 @@ extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint
   }
   return launch_layernorm(cur, wts + lay.final_off, wts + lay.final_off + align64(D), mask,
                           (half*)y, T, D, 1e-5f, stream);
+}
+
+}  // namespace tt
+
+extern "C" int tt_transformer_fwd(const void* weights, const void* x, const uint8_t* mask, void* y,
+                                  void* workspace, int64_t workspace_bytes, int batch, int seq,
+                                  int d_model, int num_heads, int ffn_dim, int num_layers,
+                                  int causal, int plan, void* stream) {
+  return transformer_fwd(weights, x, mask, y, workspace, workspace_bytes, batch, seq, d_model,
+                         num_heads, ffn_dim, num_layers, causal, plan, false, stream);
+}
+
+extern "C" int tt_megakernel_error_offset(int batch, int seq, int d_model, int num_heads,
+                                          int ffn_dim, int num_layers, int64_t* offset) {
+  int rc = check_model_shape(batch, seq, d_model, num_heads, ffn_dim, num_layers);
+  if (rc != TT_OK) return rc;
+  TT_REQUIRE(offset != nullptr, "megakernel_error_offset: null output");
+  *offset = (int64_t)megakernel_error_offset(batch, seq, d_model, ffn_dim, num_layers);
+  return TT_OK;
+}
+
+extern "C" int tt_megakernel_attach_status(void* workspace, int64_t workspace_bytes, int batch,
+                                           int seq, int d_model, int num_heads, int ffn_dim,
+                                           int num_layers, int32_t* host_status, void* stream) {
+  int rc = check_model_shape(batch, seq, d_model, num_heads, ffn_dim, num_layers);
+  if (rc != TT_OK) return rc;
+  TT_REQUIRE(workspace != nullptr, "megakernel_attach_status: null workspace");
+  return megakernel_attach_status(workspace, workspace_bytes, batch, seq, d_model, num_heads,
+                                  ffn_dim, num_layers, (uint32_t*)host_status,
+                                  (hipStream_t)stream);
+}
+
+extern "C" int tt_megakernel_set_spin_limit(int64_t limit) {
+  megakernel_set_spin_limit(limit);
+  return TT_OK;
 }

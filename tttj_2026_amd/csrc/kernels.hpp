@@ -47,6 +47,26 @@ int launch_megakernel(const half* weights, const int64_t off[12], int64_t stride
 int megakernel_tasks(int B, int S, int D, int H, int F, int L);
 int megakernel_status(const char* workspace, int B, int S, int D, int F, int L, int* status,
                       hipStream_t stream);
+// Byte offset of the 32-bit error word (non-zero once a dependency wait gave up) in the workspace.
+size_t megakernel_error_offset(int B, int S, int D, int F, int L);
+// Zero the dependency counters and control words of a megakernel workspace with a fill kernel (no
+// memset node, so the call may be captured into a graph); the next launch is then epoch 1.
+int megakernel_reset(void* workspace, int64_t workspace_bytes, int B, int S, int D, int H, int F,
+                     int L, hipStream_t stream);
+// Store the address of a pinned host word into the workspace's control area (stream-ordered); at
+// the end of every later launch the last workgroup writes the error flag there (0 or 1).
+int megakernel_attach_status(void* workspace, int64_t workspace_bytes, int B, int S, int D, int H,
+                             int F, int L, uint32_t* host_status, hipStream_t stream);
+// Polls per dependency wait before it gives up, for later launches (< 0: the default).
+void megakernel_set_spin_limit(int64_t limit);
+
+// The whole forward (tt_transformer_fwd's body, forward.hip) on the given workspace; with
+// reset_counters the megakernel plan first clears its dependency counters (a workspace shared
+// with calls of other shapes).
+int transformer_fwd(const void* weights, const void* x, const uint8_t* mask, void* y,
+                    void* workspace, int64_t workspace_bytes, int batch, int seq, int d_model,
+                    int num_heads, int ffn_dim, int num_layers, int causal, int plan,
+                    bool reset_counters, void* stream);
 
 // LayerNorm-prologue GEMM tiles (megakernel.hip): Y = LN(x) W^T + b for 64 x 64 tiles with the
 // TT_EPI_QKV or TT_EPI_BIAS_GELU epilogue, D <= 512.

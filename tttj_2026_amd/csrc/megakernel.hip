@@ -50,7 +50,7 @@ constexpr int kQB = 128;           // queries per attention block (= attention_b
 constexpr int kNB = 64;            // columns per GEMM tile
 constexpr int kMaxD = 512;         // LN'd A operand resident in LDS: 64 x D halfs
 constexpr int kMKThreads = 256;
-constexpr uint32_t kSpinLimit = 1u << 22;
+constexpr uint32_t kSpinLimit = 1u << 22;  // polls (each followed by s_sleep 1) per wait
 
 // LDS map (halfs), 144 KiB + a small int area at the end.  Tasks whose A operand is a
 // LayerNorm computed in LDS (QKV, FF1) use [0, kResA) for it and a ring of kRingW weight-only K
@@ -75,8 +75,10 @@ struct MegaParams {
   const uint8_t* mask;
   half *xa, *ctx, *q, *k, *vt, *hbuf;
   uint32_t* cnt;    // [L * kNumCounters * nrb]
-  uint32_t* ctrl;   // [0] epoch, [1] finished workgroups, [2] error flag
+  uint32_t* ctrl;   // [0] epoch, [1] finished workgroups, [2] error flag, [4..5] host mirror
+                    // address of the error flag (0: none), set by megakernel_attach_status
   uint64_t* trace;  // optional: 4 words per task (task | wg << 32, start, ready, end) or nullptr
+  uint32_t spin_limit;  // polls per dependency wait before it gives up (kSpinLimit by default)
   int B, S, D, H, F, L, causal;
   int nsb, nqb, nrb, tq, td, tf;  // row / query blocks per sequence, row blocks, N tiles
   int per_layer, ntask;
@@ -110,7 +112,7 @@ __device__ void mk_wait(const MegaParams& p, const uint32_t* c, uint32_t target)
     uint32_t spins = 0;
     while ((int32_t)(ld_relaxed(c) - target) < 0) {
       if (ld_relaxed(p.ctrl + 2) != 0) break;  // an earlier wait expired: fall through
-      if (++spins > kSpinLimit) {
+      if (++spins > p.spin_limit) {
         __hip_atomic_store(p.ctrl + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
@@ -589,14 +591,32 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
 
   // The last workgroup to finish advances the epoch for the next launch and clears the
   // finish count (every workgroup read the epoch before it arrives here; the next launch is
-  // stream-ordered after this one).
+  // stream-ordered after this one).  If a dependency wait of this or an earlier launch gave up
+  // (error word set), the results are invalid: that workgroup then overwrites all of y with NaN
+  // (fp16 0x7E00) -- the arrivals are acq_rel, so every other workgroup's writes of y precede it
+  // -- and the host sees the error word on its next health check.
+  __shared__ uint32_t last;
   __syncthreads();
   if (threadIdx.x == 0) {
+    last = 0;
     const uint32_t old = __hip_atomic_fetch_add(p.ctrl + 1, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (old + 1u == gridDim.x) {
       __hip_atomic_store(p.ctrl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(p.ctrl, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t err = ld_relaxed(p.ctrl + 2);
+      last = err != 0 ? 1u : 0u;
+      // mirror the error flag into the caller's pinned host word, if one is attached
+      const uint64_t host = __hip_atomic_load((const uint64_t*)(p.ctrl + 4), __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+      if (host != 0)
+        __hip_atomic_store((uint32_t*)host, err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
+  }
+  __syncthreads();
+  if (last) {
+    const size_t n8 = (size_t)p.B * p.S * p.D / 8;  // D % 64 == 0
+    const u32x4 nan8 = {0x7E007E00u, 0x7E007E00u, 0x7E007E00u, 0x7E007E00u};
+    for (size_t i = threadIdx.x; i < n8; i += blockDim.x) *(u32x4*)(p.y + 8 * i) = nan8;
   }
 }
 
@@ -709,6 +729,16 @@ int megakernel_tasks(int B, int S, int D, int H, int F, int L) {
   return L * per_layer + nrb;
 }
 
+size_t megakernel_error_offset(int B, int S, int D, int F, int L) {
+  return mega_layout(B, S, D, F, L).ctrl + 2 * sizeof(uint32_t);
+}
+
+static uint32_t g_spin_limit = kSpinLimit;
+
+void megakernel_set_spin_limit(int64_t limit) {
+  g_spin_limit = limit < 0 ? kSpinLimit : (uint32_t)std::min<int64_t>(limit, 0xFFFFFFFFll);
+}
+
 int launch_megakernel(const half* weights, const int64_t off[12], int64_t stride, int64_t final_off,
                       const half* x, const uint8_t* mask, half* y, char* workspace,
                       int64_t workspace_bytes, int B, int S, int D, int H, int F, int L, int causal,
@@ -735,6 +765,7 @@ int launch_megakernel(const half* weights, const int64_t off[12], int64_t stride
   p.cnt = (uint32_t*)(workspace + m.cnt);
   p.ctrl = (uint32_t*)(workspace + m.ctrl);
   p.trace = trace;
+  p.spin_limit = g_spin_limit;
   p.B = B;
   p.S = S;
   p.D = D;
@@ -754,6 +785,43 @@ int launch_megakernel(const half* weights, const int64_t off[12], int64_t stride
   const int hd = D / H;
   if (hd == 64) return causal ? launch_mega<64, true>(p, stream) : launch_mega<64, false>(p, stream);
   return causal ? launch_mega<32, true>(p, stream) : launch_mega<32, false>(p, stream);
+}
+
+__global__ void mk_zero_words(uint32_t* __restrict__ p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+int megakernel_reset(void* workspace, int64_t workspace_bytes, int B, int S, int D, int H, int F,
+                     int L, hipStream_t stream) {
+  int rc = megakernel_supported(B, S, D, H, F, L);
+  if (rc != TT_OK) return rc;
+  const MegaLayout m = mega_layout(B, S, D, F, L);
+  TT_REQUIRE((int64_t)m.bytes <= workspace_bytes, "megakernel: workspace %lld < %zu bytes",
+             (long long)workspace_bytes, m.bytes);
+  // counters and control words are contiguous: [cnt, ctrl + 64)
+  const size_t words = (m.ctrl + 64 - m.cnt) / 4;
+  const int blocks = (int)std::min<size_t>((words + 255) / 256, 1024);
+  hipLaunchKernelGGL(mk_zero_words, dim3(blocks), dim3(256), 0, stream,
+                     (uint32_t*)((char*)workspace + m.cnt), words);
+  return launch_status("mk_zero_words");
+}
+
+__global__ void mk_set_word64(uint64_t* __restrict__ dst, uint64_t value) {
+  if (threadIdx.x == 0) *dst = value;
+}
+
+int megakernel_attach_status(void* workspace, int64_t workspace_bytes, int B, int S, int D, int H,
+                             int F, int L, uint32_t* host_status, hipStream_t stream) {
+  int rc = megakernel_supported(B, S, D, H, F, L);
+  if (rc != TT_OK) return rc;
+  const MegaLayout m = mega_layout(B, S, D, F, L);
+  TT_REQUIRE((int64_t)m.bytes <= workspace_bytes, "megakernel: workspace %lld < %zu bytes",
+             (long long)workspace_bytes, m.bytes);
+  hipLaunchKernelGGL(mk_set_word64, dim3(1), dim3(64), 0, stream,
+                     (uint64_t*)((char*)workspace + m.ctrl + 4 * sizeof(uint32_t)),
+                     (uint64_t)(uintptr_t)host_status);
+  return launch_status("mk_set_word64");
 }
 
 int megakernel_status(const char* workspace, int B, int S, int D, int F, int L, int* status,

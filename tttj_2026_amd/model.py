@@ -83,7 +83,7 @@ class BaselineSelfAttention(nn.Module):
         q, k, v = (self._heads(p(x)) for p in (self.q_proj, self.k_proj, self.v_proj))
         # Eager semantics (:97-117): scores in the activation dtype, scaled, masked with -inf,
         # softmax in fp32, probabilities cast back, then P.V.
-        scores = torch.matmul(q, k.transpose(-2, -1).contiguous()) * self.scale
+        scores = torch.matmul(q, k.transpose(-2, -1)) * self.scale
         if causal:
             upper = torch.ones((s, s), device=x.device, dtype=torch.bool).triu(diagonal=1)
             scores = scores.masked_fill(upper, float("-inf"))

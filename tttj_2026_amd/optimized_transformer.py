@@ -14,15 +14,23 @@ current stream: either the layer-wise plan (LN, four GEMMs with fused epilogues 
 layer) or, for small token counts, the persistent megakernel (one launch for the whole
 stack, workgroups handing work to each other through dependency counters); ``plan`` forces one.
 It returns a fresh output tensor per call; repeated calls on the same inputs are bit-identical.
-A module instance owns one workspace per (batch, seq, plan) -- for the megakernel it holds the
-dependency counters and launch epoch, so it is zero-filled once and then reused -- and is not
-re-entrant across streams (the reference's scheduler buffer has the same contract,
-kernels/sequence_resident.py:148-150).
+A module instance owns one scratch workspace per device for the layer-wise plans (grown to the
+largest shape seen and reused for smaller ones) and a few megakernel workspaces (the most recent
+``MEGA_WORKSPACES_KEPT`` (batch, seq) shapes; each holds that shape's dependency counters and launch
+epoch, so it is zero-filled once and then reused), and is not re-entrant across streams (the
+reference's scheduler buffer has the same contract, kernels/sequence_resident.py:148-150).
+
+The megakernel's dependency waits are bounded; a wait that gives up makes that launch write NaN
+over its output and sets an error flag that the kernel mirrors into a pinned host word.  The next
+``forward`` on that shape reads the word (host memory, no synchronisation) and raises
+``MegakernelWaitError`` after re-arming the workspace, so one expiry never turns into silently
+wrong results.
 """
 
 from __future__ import annotations
 
 import ctypes
+from collections import OrderedDict
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -36,6 +44,14 @@ PLAN_AUTO, PLAN_LAYERWISE, PLAN_MEGAKERNEL, PLAN_FUSED_LN = (
 
 
 SUPPORTED_HEAD_DIMS = (8, 16, 32, 64, 128, 256)
+
+# Megakernel workspaces kept per module (least recently used ones are dropped beyond this).
+MEGA_WORKSPACES_KEPT = 4
+
+
+class MegakernelWaitError(RuntimeError):
+    """A dependency wait of the persistent megakernel gave up (the device did not run all of its
+    workgroups at once, e.g. because other kernels held CUs); that launch's output was NaN."""
 
 # The reference's public case table under its own names (optimized_transformer.py:22-42); this
 # build accepts those shapes and more (check_supported), the table is kept for callers that use it.
@@ -138,7 +154,14 @@ class OptimizedTransformer(nn.Module):
         self.config = parameter_model.config
         self.plan = plan
         self.register_buffer("packed_weights", None, persistent=False)
-        self._workspaces: Dict[Tuple[int, int, int, int], torch.Tensor] = {}
+        # layer-wise plans: one scratch buffer per device, grown to the largest shape seen
+        self._scratch: Dict[int, torch.Tensor] = {}
+        # megakernel plan: (batch, seq, device) -> (workspace, pinned host error word, its numpy
+        # view)
+        self._mega: "OrderedDict[Tuple[int, int, int], Tuple[torch.Tensor, torch.Tensor]]" = \
+            OrderedDict()
+        self._nbytes: Dict[Tuple[int, int, int], int] = {}
+        self.last_workspace: Optional[torch.Tensor] = None
 
     def prepare(self) -> None:
         check_supported(self.config)
@@ -147,16 +170,64 @@ class OptimizedTransformer(nn.Module):
         self._lib = lib
 
     def _workspace(self, batch: int, seq: int, plan: int, device: torch.device) -> torch.Tensor:
-        key = (batch, seq, plan, device.index if device.index is not None else 0)
-        ws = self._workspaces.get(key)
-        if ws is None:
-            cfg = self.config
+        cfg = self.config
+        nbytes = self._nbytes.get((batch, seq, plan))
+        if nbytes is None:
             nbytes = _lib.workspace_bytes(batch, seq, cfg.d_model, cfg.num_heads, cfg.ffn_dim,
                                           cfg.num_layers, plan)
-            # zero-filled: the megakernel's dependency counters and epoch must start at 0
+            if len(self._nbytes) >= 256:
+                self._nbytes.clear()
+            self._nbytes[(batch, seq, plan)] = nbytes
+        dev = device.index if device.index is not None else 0
+        if plan == PLAN_MEGAKERNEL:
+            return self._mega_entry(batch, seq, dev, nbytes, device)[0]
+        ws = self._scratch.get(dev)
+        if ws is None or ws.numel() < nbytes:
+            # the previous buffer is released here unless a captured graph still holds it
             ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-            self._workspaces[key] = ws
+            self._scratch[dev] = ws
         return ws
+
+    def _mega_entry(self, batch, seq, dev, nbytes, device):
+        key = (batch, seq, dev)
+        entry = self._mega.pop(key, None)
+        if entry is None:
+            # zero-filled: the dependency counters and epoch must start at 0
+            ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+            status = self._new_status_word()
+            entry = (ws, status, status.numpy())  # the numpy view reads host memory cheaply
+            self._attach(entry, batch, seq)
+        self._mega[key] = entry  # most recently used last
+        while len(self._mega) > MEGA_WORKSPACES_KEPT:
+            self._mega.popitem(last=False)
+        return entry
+
+    @staticmethod
+    def _new_status_word() -> torch.Tensor:
+        return torch.zeros(1, dtype=torch.int32, pin_memory=True)
+
+    def _attach(self, entry, batch, seq) -> None:
+        ws, status, _ = entry
+        cfg = self.config
+        _lib.check(self._lib.tt_megakernel_attach_status(
+            ws.data_ptr(), ws.numel(), batch, seq, cfg.d_model, cfg.num_heads, cfg.ffn_dim,
+            cfg.num_layers, status.data_ptr(),
+            torch.cuda.current_stream(ws.device).cuda_stream), "tt_megakernel_attach_status")
+
+    def _check_mega_health(self, entry, batch, seq) -> None:
+        """Raise MegakernelWaitError if an earlier launch on this workspace reported a wait that
+        gave up (its output was NaN), after re-arming the workspace: synchronise, zero-fill,
+        re-attach the host word and clear it."""
+        ws, status, word = entry
+        if word[0] == 0:
+            return
+        torch.cuda.current_stream(ws.device).synchronize()  # no launch may still write the word
+        ws.zero_()
+        status[0] = 0
+        self._attach(entry, batch, seq)
+        raise MegakernelWaitError(
+            "megakernel: a dependency wait gave up in an earlier forward on this shape (its "
+            "output was NaN); the workspace has been reset")
 
     def forward_traced(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None):
         """Megakernel forward that also returns its per-task trace: an int64 [tasks, 4] CPU
@@ -189,12 +260,12 @@ class OptimizedTransformer(nn.Module):
         far, 1 if one exceeded its bound (synchronises the current stream)."""
         cfg = self.config
         dev = self.packed_weights.device
-        ws = self._workspaces.get((batch, seq, PLAN_MEGAKERNEL, dev.index or 0))
-        if ws is None:
+        entry = self._mega.get((batch, seq, dev.index or 0))
+        if entry is None:
             return 0
         status = ctypes.c_int(0)
         _lib.check(self._lib.tt_megakernel_status(
-            ws.data_ptr(), batch, seq, cfg.d_model, cfg.ffn_dim, cfg.num_layers,
+            entry[0].data_ptr(), batch, seq, cfg.d_model, cfg.ffn_dim, cfg.num_layers,
             ctypes.byref(status), torch.cuda.current_stream(dev).cuda_stream),
             "tt_megakernel_status")
         return status.value
@@ -224,6 +295,9 @@ class OptimizedTransformer(nn.Module):
             return y
         plan = _lib.resolve_plan(batch, seq, cfg.d_model, cfg.num_heads, cfg.ffn_dim, self.plan)
         ws = self._workspace(batch, seq, plan, x.device)
+        if plan == PLAN_MEGAKERNEL:
+            self._check_mega_health(self._mega[(batch, seq, x.device.index or 0)], batch, seq)
+        self.last_workspace = ws
         stream = torch.cuda.current_stream(x.device).cuda_stream
         rc = self._lib.tt_transformer_fwd(
             self.packed_weights.data_ptr(), x.data_ptr(), mask_ptr, y.data_ptr(), ws.data_ptr(),
@@ -261,6 +335,7 @@ class GraphedOptimizedTransformer(nn.Module):
         self._static_input: Optional[torch.Tensor] = None
         self._static_mask: Optional[torch.Tensor] = None
         self._static_output: Optional[torch.Tensor] = None
+        self._static_workspace: Optional[torch.Tensor] = None
 
     @staticmethod
     def _signature(x: torch.Tensor, mask: Optional[torch.Tensor]):
@@ -284,6 +359,9 @@ class GraphedOptimizedTransformer(nn.Module):
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph), torch.inference_mode():
             out = self.module(x, valid_token_mask)
+        # the graph replays on this workspace: keep it alive even if the module later grows or
+        # drops its own buffers
+        self._static_workspace = self.module.last_workspace
         self._graph = graph
         self._key = self._signature(x, valid_token_mask)
         self._static_input, self._static_mask, self._static_output = x, valid_token_mask, out
