@@ -197,6 +197,23 @@ int tt_transformer_fwd(const void* weights, const void* x, const uint8_t* mask, 
                        int num_heads, int ffn_dim, int num_layers, int causal, int plan,
                        void* stream);
 
+/* Size in bytes of the scratch array tt_transformer_fwd_noalloc works in (64 MiB). */
+int tt_noalloc_scratch_bytes(int64_t* bytes);
+
+/* tt_transformer_fwd without a workspace argument and without any allocation.  No counterpart in
+ * the reference: it exists for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The intermediates live in a
+ * fixed scratch array of the library (tt_noalloc_scratch_bytes, 64 MiB), one per GPU, which the
+ * runtime allocates when the library's code object is loaded on that GPU and keeps until the
+ * process ends; shapes that need more (tt_workspace_bytes) fail with TT_ERR_INVALID before any
+ * launch.  Same arguments, plans and results as tt_transformer_fwd.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (other streams, threads) race on it, so order
+ * them on one stream.  The megakernel plan clears its dependency counters at the start of each
+ * call (a fill kernel, no memset). */
+int tt_transformer_fwd_noalloc(const void* weights, const void* x, const uint8_t* mask, void* y,
+                               int batch, int seq, int d_model, int num_heads, int ffn_dim,
+                               int num_layers, int causal, int plan, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

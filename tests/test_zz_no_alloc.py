@@ -1,0 +1,84 @@
+"""tt_transformer_fwd_noalloc (the forward on the library's own scratch array, no allocation)
+against tt_transformer_fwd on a caller workspace, through the C ABI.
+
+Both run the same kernels, so outputs must be bit-identical.  Two calls in a row share the
+scratch array, the second with a smaller input (it must not be disturbed by what the first
+left there), for the layer-wise and the megakernel plans; a shape whose intermediates exceed the
+array is rejected with an argument error before any launch.
+"""
+
+import copy
+import ctypes
+
+import pytest
+import torch
+
+from tttj_2026_amd import PLAN_AUTO, PLAN_MEGAKERNEL, _lib, make_optimized_transformer
+from tttj_2026_amd.configs import build_model, make_inputs
+from tttj_2026_amd.model import TransformerConfig
+
+pytestmark = pytest.mark.gpu
+
+_P, _I, _I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+
+
+def _lib_noalloc():
+    return _lib.load()
+
+
+def _run_pair(device, lib, cfg_model, shape, plan, masked, seed):
+    """Output of the no-alloc entry point and of tt_transformer_fwd for one (B, S) input."""
+    b, s = shape
+    gm, opt = cfg_model
+    cfg = gm.config
+    run_cfg = TransformerConfig(b, s, cfg.d_model, cfg.num_heads, cfg.ffn_dim, cfg.num_layers,
+                                cfg.causal)
+    x16, mask = make_inputs(run_cfg, masked, seed, min_valid=max(1, s // 3))
+    xd = x16.to(device)
+    md = mask.to(device) if masked else None
+    stream = torch.cuda.current_stream(device).cuda_stream
+    y_na = torch.full_like(xd, float("nan"))
+    print(f"[noalloc] plan {plan} B{b} S{s} D{cfg.d_model} masked={masked}", flush=True)
+    rc = lib.tt_transformer_fwd_noalloc(
+        opt.packed_weights.data_ptr(), xd.data_ptr(), None if md is None else md.data_ptr(),
+        y_na.data_ptr(), b, s, cfg.d_model, cfg.num_heads, cfg.ffn_dim, cfg.num_layers,
+        int(cfg.causal), plan, stream)
+    _lib.check(rc, "tt_transformer_fwd_noalloc")
+    nbytes = _lib.workspace_bytes(b, s, cfg.d_model, cfg.num_heads, cfg.ffn_dim, cfg.num_layers,
+                                  plan)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+    y_ref = torch.empty_like(xd)
+    rc = lib.tt_transformer_fwd(
+        opt.packed_weights.data_ptr(), xd.data_ptr(), None if md is None else md.data_ptr(),
+        y_ref.data_ptr(), ws.data_ptr(), nbytes, b, s, cfg.d_model, cfg.num_heads, cfg.ffn_dim,
+        cfg.num_layers, int(cfg.causal), plan, stream)
+    _lib.check(rc, "tt_transformer_fwd")
+    torch.cuda.synchronize()
+    return y_na, y_ref
+
+
+@pytest.mark.parametrize("plan", [PLAN_AUTO, PLAN_MEGAKERNEL], ids=["auto", "megakernel"])
+def test_noalloc_matches_workspace_entry(device, plan):
+    lib = _lib_noalloc()
+    cfg = TransformerConfig(4, 128, 256, 4, 1024, 2, True)
+    gm = build_model(cfg, seed=21).half().to(device).eval()
+    opt = make_optimized_transformer(copy.deepcopy(gm))
+    # first call, then a smaller one with a mask: both bit-identical to the workspace entry point
+    for shape, masked, seed in (((4, 128), False, 22), ((2, 77), True, 23)):
+        y_na, y_ref = _run_pair(device, lib, (gm, opt), shape, plan, masked, seed)
+        assert torch.isfinite(y_ref).all()
+        assert torch.equal(y_na, y_ref), shape
+
+
+def test_noalloc_rejects_shapes_beyond_scratch(device):
+    lib = _lib_noalloc()
+    cap = _I64()
+    assert lib.tt_noalloc_scratch_bytes(ctypes.byref(cap)) == 0
+    need = _lib.workspace_bytes(2, 4096, 1024, 16, 4096, 12, PLAN_AUTO)  # C5: 144 MiB
+    assert need > cap.value
+    y = torch.empty(1, device=device, dtype=torch.float16)
+    rc = lib.tt_transformer_fwd_noalloc(y.data_ptr(), y.data_ptr(), None, y.data_ptr() + 2, 2,
+                                        4096, 1024, 16, 4096, 12, 1, PLAN_AUTO,
+                                        torch.cuda.current_stream(device).cuda_stream)
+    assert rc == _lib.TT_ERR_INVALID
+    assert "scratch" in _lib.last_error()

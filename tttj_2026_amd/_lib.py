@@ -44,6 +44,8 @@ SIGNATURES = {
     "tt_mask_info": (_I, [_P, _P, _I, _I, _P]),
     "tt_attention_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "tt_transformer_fwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "tt_noalloc_scratch_bytes": (_I, [ctypes.POINTER(_I64)]),
+    "tt_transformer_fwd_noalloc": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
 }
 
 _lock = threading.Lock()
