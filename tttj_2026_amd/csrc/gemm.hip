@@ -144,12 +144,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const half* base, 
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, bytes, 0x00020000);
 }
 
-template <int BM, int BN, int MODE, int PATH>
-__global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
-                                                   const half* __restrict__ W, int M, int N, int K,
-                                                   EpiArgs ep) {
-  // 2 x 2 waves, each owning a (BM/2) x (BN/2) block of C as FM x FN 32x32 MFMA tiles.
-  constexpr int WM = BM / 2, WN = BN / 2;
+// Blocks of NW waves (4: a 2 x 2 wave grid; 8: 4 x 2, i.e. four waves along M), each wave owning
+// a (BM / (NW / 2)) x (BN / 2) block of C as FM x FN 32x32 MFMA tiles.  Two 4-wave blocks of up to
+// 128 x 128 share a CU (one's epilogue runs beside the other's main loop); an 8-wave block puts two
+// waves on every SIMD by itself.
+template <int BM, int BN, int MODE, int PATH, int NW = 4>
+__global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1) void gemm_kernel(
+    const half* __restrict__ X, const half* __restrict__ W, int M, int N, int K, EpiArgs ep) {
+  constexpr int WGM = NW / 2;
+  constexpr int WM = BM / WGM, WN = BN / 2;
   constexpr int FM = WM / 32, FN = WN / 32;
   constexpr int ROWS = BM + BN;       // LDS rows per stage: X rows [0, BM), W rows [BM, BM + BN)
   // LDS row stride in halfs: 128-byte rows with XOR-swizzled chunks for the direct copies (one
@@ -158,11 +161,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
   // in 16 different bank groups.
   constexpr int LDR = PATH ? kBK + 8 : kBK;
   constexpr int STAGE = ROWS * LDR;   // halfs per stage
-  constexpr int XL = BM / 32;         // X copies per wave per stage (8 rows x 4 waves each)
-  constexpr int WL = BN / 32;         // W copies per wave per stage
+  static_assert(PATH == 0 || NW == 4, "the register path is laid out for 4 waves");
+  constexpr int XL = BM / (8 * NW);   // X copies per wave per stage (8 rows each)
+  constexpr int WL = BN / (8 * NW);   // W copies per wave per stage
   constexpr int NL = XL + WL;
   constexpr int KSUB = kBK / 16;      // MFMA k-steps per stage
-  constexpr int CSPREAD = KSUB / 2;
+  static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "copy split");
 
   extern __shared__ __align__(16) half lds[];
 
@@ -215,100 +219,92 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half* __restrict__ X,
   };
 
   if constexpr (PATH == 0) {
-    // Copy sources: copy i of this wave fills 8-row group wave + 4 i of the stage.  X rows past M
+    // Copy sources: copy i of this wave fills 8-row group wave + NW i of the stage.  X rows past M
     // are clamped to M - 1 (valid memory whose results are never stored).
     // Offsets are relative to the block's first X row and W row (64-bit bases), so M * K may
     // exceed 2^31 (long sequences); BM * K and BN * K stay far below it.
     // Chunk layout: physical chunk = logical ^ bits 1-3 of the row, so that the 16 consecutive rows
     // one ds_read_b128 phase reads land in 16 different bank groups (with bits 0-2, rows r and
-    // r + 8 would share banks).  Row (wave + 4 i) * 8 + lrow has bits 1-3 = (wave & 1) << 2 |
-    // lrow >> 1 for every i.
+    // r + 8 would share banks).  Row (wave + NW i) * 8 + lrow has bits 1-3 = (wave & 1) << 2 |
+    // lrow >> 1 for every i (NW is even).
     const int lrow = lane >> 3, lchunk = (lane & 7) ^ (((wave & 1) << 2) | (lrow >> 1));
     const half* Xb = X + (size_t)m0 * K;
     const half* Wb = W + (size_t)n0 * K;
+    const int nk = K / kBK;
     int src_off[NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-      const int r = (wave + 4 * i) * 8 + lrow;
+      const int r = (wave + NW * i) * 8 + lrow;
       if (i < XL) src_off[i] = min(r, M - 1 - m0) * K + lchunk * 8;
       else src_off[i] = (r - BM) * K + lchunk * 8;
     }
     // The wave index is made provably uniform so the LDS destination (M0) is scalar arithmetic;
     // the source is a uniform base advanced by k0 plus the lane's fixed 32-bit offset, which
-    // lets the copy use the scalar-base addressing mode (no per-copy 64-bit VALU adds).
+    // lets the copy use the scalar-base addressing mode (no per-copy 64-bit VALU adds).  Copies
+    // of stages past the last one re-read the last stage into the buffer nobody reads any more,
+    // so that no copy sits behind a branch: every k-step below is one basic block, which the
+    // interleaving hints need.
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    auto copy = [&](int i, int k0, half* stage) {
-      const half* base = ((i < XL) ? Xb : Wb) + k0;
-      lds_copy16(base + (uint32_t)src_off[i], stage + (wave_u + 4 * i) * 8 * kBK);
+    auto copy = [&](int i, int kt, half* stage) {
+      const half* base = ((i < XL) ? Xb : Wb) + min(kt, nk - 1) * kBK;
+      lds_copy16(base + (uint32_t)src_off[i], stage + (wave_u + NW * i) * 8 * kBK);
     };
 
-    // One stage: KSUB k-steps of FN x FM MFMAs.  Fragment reads for k-step kk + 1 and (MORE) the
-    // copies of the next stage are interleaved one per MFMA.
-    auto stage = [&](auto more_tag, const half* cur, half* nxt, int k1) {
-      constexpr bool MORE = decltype(more_tag)::value;
+    // Copies of the next stage per k-step: C0 in the first (they have the whole stage to land),
+    // the rest spread evenly over the others, so that no wave issues a burst of copies (each one
+    // holds the wave's issue for ~100 cycles when the CU's copy queue is busy).  An 8-wave block
+    // issues all of them at once: the other wave of the SIMD keeps the MFMAs busy meanwhile.
+    constexpr int C0 = NW == 8 ? NL : (NL + 3) / 4;
+    constexpr int CPER = (NL - C0 + KSUB - 2) / (KSUB - 1);
+    // One stage: KSUB k-steps of FN x FM MFMAs; the next k-step's fragment reads and this
+    // k-step's copies of stage kn are interleaved one per MFMA.
+    auto stage = [&](const half* cur, half* nxt, int kn) {
       frags(0, 0, cur);
 #pragma unroll
       for (int kk = 0; kk < KSUB; ++kk) {
         __builtin_amdgcn_sched_barrier(0);
         if (kk + 1 < KSUB) frags((kk + 1) & 1, kk + 1, cur);
-        // The next stage's copies go out during the first CSPREAD k-steps, so they have most of
-        // the stage to land before the end-of-stage wait.
-        const int c_lo = kk < CSPREAD ? kk * NL / CSPREAD : NL;
-        const int c_hi = kk < CSPREAD ? (kk + 1) * NL / CSPREAD : NL;
-        if constexpr (MORE) {
+        const int c_lo = kk == 0 ? 0 : min(NL, C0 + (kk - 1) * CPER);
+        const int c_hi = kk == 0 ? C0 : min(NL, C0 + kk * CPER);
 #pragma unroll
-          for (int c = c_lo; c < c_hi; ++c) copy(c, k1, nxt);
-        }
+        for (int c = c_lo; c < c_hi; ++c) copy(c, kn, nxt);
 #pragma unroll
         for (int i = 0; i < FN; ++i)
 #pragma unroll
           for (int j = 0; j < FM; ++j)
             acc[i][j] = mfma32x32x16(af[kk & 1][i], bf[kk & 1][j], acc[i][j]);
-        if (kk + 1 < KSUB) {
+        const int nds = kk + 1 < KSUB ? FN + FM : 0;
 #pragma unroll
-          for (int t = 0; t < FN + FM; ++t) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          }
+        for (int t = 0; t < FN * FM; ++t) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // MFMA
+          if (t < nds) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // DS read
+          if (t < c_hi - c_lo) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // copy
         }
-        if constexpr (MORE) {
-#pragma unroll
-          for (int c = c_lo; c < c_hi; ++c) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-          }
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, FN * FM, 0);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
 
-    const int nk = K / kBK;
-    // Prologue: stage 0.
+    // Prologue: stage 0.  Then two stages per iteration, so both buffers are constant offsets
+    // (fragment reads use immediate offsets).  Before each stage: its copies have landed in LDS
+    // (vmcnt 0: every copy of this wave is older than the ones the stage issues) and every wave
+    // is done reading the buffer the stage's own copies overwrite.
 #pragma unroll
     for (int i = 0; i < NL; ++i) copy(i, 0, lds);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    // Unrolled by two so that both stage buffers are constant offsets (fragment reads then use
-    // immediate offsets instead of one address add each).  After each stage: the next stage's
-    // copies have landed in LDS and every wave is done reading this one.
     int kt = 0;
-    for (; kt + 2 < nk; kt += 2) {
-      stage(std::true_type{}, lds, lds + STAGE, (kt + 1) * kBK);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      stage(std::true_type{}, lds + STAGE, lds, (kt + 2) * kBK);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
+    for (; kt + 2 <= nk; kt += 2) {
+      wait_vmcnt<0>();
+      raw_barrier();
+      stage(lds, lds + STAGE, kt + 1);
+      wait_vmcnt<0>();
+      raw_barrier();
+      stage(lds + STAGE, lds, kt + 2);
     }
-    if (kt + 1 < nk) {  // two stages left (kt is even: stage kt is in the first buffer)
-      stage(std::true_type{}, lds, lds + STAGE, (kt + 1) * kBK);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      stage(std::false_type{}, lds + STAGE, nullptr, 0);
-    } else {
-      stage(std::false_type{}, lds, nullptr, 0);
+    if (kt < nk) {
+      wait_vmcnt<0>();
+      raw_barrier();
+      stage(lds, lds + STAGE, kt + 1);
     }
+    wait_vmcnt<0>();  // the re-read copies past the end land before the epilogue reuses LDS
 
   } else {
     // Register path.  Thread t moves chunk t % 8 of rows t / 8 + 32 i (i < RX: X rows, then W
@@ -749,24 +745,23 @@ struct TileCfg {
   int bm, bn;
 };
 
-template <int BM, int BN, int MODE, int PATH>
+template <int BM, int BN, int MODE, int PATH, int NW = 4>
 static int run_tile(const half* x, const half* w, int m, int n, int k, const EpiArgs& ep,
                     hipStream_t stream) {
-  constexpr int NT = 256;
   // double-buffered K stages; the epilogue stages the whole BM x BN tile in the same memory
   const size_t lds = std::max(2 * (size_t)(BM + BN) * (PATH ? kBK + 8 : kBK), (size_t)BM * BN) *
                      sizeof(half);
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
   std::call_once(once, [&] {
-    attr_err = hipFuncSetAttribute((const void*)gemm_kernel<BM, BN, MODE, PATH>,
+    attr_err = hipFuncSetAttribute((const void*)gemm_kernel<BM, BN, MODE, PATH, NW>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   });
   if (attr_err != hipSuccess)
     return fail(TT_ERR_HIP, "hipFuncSetAttribute(gemm %dx%d): %s", BM, BN, hipGetErrorString(attr_err));
   const int tiles = ((m + BM - 1) / BM) * (n / BN);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, MODE, PATH>), dim3(tiles), dim3(NT), lds, stream, x, w,
-                     m, n, k, ep);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, MODE, PATH, NW>), dim3(tiles), dim3(64 * NW), lds,
+                     stream, x, w, m, n, k, ep);
   return launch_status("gemm_kernel");
 }
 
@@ -774,7 +769,7 @@ template <int MODE>
 static int run_mode(int tile, const half* x, const half* w, int m, int n, int k, const EpiArgs& ep,
                     hipStream_t stream) {
   switch (tile) {
-    case 0: return run_tile<256, 256, MODE, 0>(x, w, m, n, k, ep, stream);
+    case 0: return run_tile<256, 256, MODE, 0, 8>(x, w, m, n, k, ep, stream);
     case 1: return run_tile<256, 128, MODE, 0>(x, w, m, n, k, ep, stream);
     case 2: return run_tile<128, 128, MODE, 0>(x, w, m, n, k, ep, stream);
     case 3: return run_tile<128, 64, MODE, 0>(x, w, m, n, k, ep, stream);
@@ -786,8 +781,9 @@ static int run_mode(int tile, const half* x, const half* w, int m, int n, int k,
   }
 }
 
-// index 5: 32 x 32 narrow tiles (gemm_narrow_kernel), chosen for grids that leave most CUs idle;
-// indices 6-9: 128 x 256, 128 x 128, 128 x 64, 256 x 128 on the register path
+// index 0: 256 x 256 on 8 waves; index 5: 32 x 32 narrow tiles (gemm_narrow_kernel), chosen for
+// grids that leave most CUs idle; indices 6-9: 128 x 256, 128 x 128, 128 x 64, 256 x 128 on the
+// register path
 static const TileCfg kTiles[] = {{256, 256}, {256, 128}, {128, 128}, {128, 64}, {64, 64},
                                  {32, 32},   {128, 256}, {128, 128}, {128, 64}, {256, 128}};
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
@@ -795,24 +791,19 @@ constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 static int g_tile_override = -1;  // test hook: force one tile configuration
 
 // Tile choice, from measurements on MI355X (M = 8192, N in {1024, 3072, 4096}, K in {1024,
-// 4096, 8192}): a 256x256 block (one per CU, 128 KiB of LDS) only pays off once K is long enough
-// to amortise its prologue and its 128 KiB epilogue (K >= 4096) and the grid still fills every CU;
-// otherwise 128x128 (two blocks per CU, so one block's epilogue overlaps the other's MFMAs) is
-// the fastest shape.  Narrower tiles are used when a wider one would leave CUs idle, down to the
-// 32x32 narrow kernel for few-token grids.
+// 4096}; round-robin medians of interleaved runs in one process): the 8-wave 256 x 256 block
+// (two waves per SIMD, half the operand traffic per FLOP of 128 x 128) wins when its tiles fill
+// whole rounds of the chip, at least two (ffn_in, 8192 x 4096 x 1024: 85 against 87 us with
+// GELU, 71 against 76 us with bias only); with 1.5 rounds (QKV, N = 3072) or half a round (N =
+// 1024) two 128 x 128 blocks per CU are faster (QKV 57 against 63 us, ffn_out 65 against 95 us).
+// Narrower tiles are used when a wider one would leave CUs idle, down to the 32x32 narrow kernel
+// for few-token grids.
 static int pick_tile(int m, int n, int k, int mode, int cus) {
+  (void)mode;
   if (g_tile_override >= 0 && g_tile_override < kNumTiles && n % kTiles[g_tile_override].bn == 0)
     return g_tile_override;
   auto tiles = [&](int i) { return (long)((m + kTiles[i].bm - 1) / kTiles[i].bm) * (n / kTiles[i].bn); };
-  if (k >= 4096 && n % 256 == 0 && tiles(0) >= cus) return 0;
-  // Register-path 128 x 128 tiles with padded LDS rows for the GELU epilogue, where they measured
-  // ahead of the direct copies (MI355X, M = 8192, N = 4096, K = 1024, medians of interleaved runs:
-  // 101.5 -> 96.7 us; two blocks per CU overlap one block's GELU with the other's MFMAs).  For the
-  // other M = 8192 projections the direct 128 x 128 tiles are as fast or faster (ffn_out,
-  // N = 1024, K = 4096, alone: 69.4 us against 73.2 for register-path 256 x 128 tiles and 73.0 for
-  // direct 256 x 128 ones; in whole forwards C5 is unchanged and C4 gains 0.8%, its padded rows
-  // filling more whole 128-row tiles than 256-row ones).
-  if (mode == TT_EPI_BIAS_GELU && n % 128 == 0 && tiles(7) >= cus) return 7;
+  if (n % 256 == 0 && tiles(0) >= 2 * cus && tiles(0) % cus == 0) return 0;
   // One round of 128 x 64 tiles streaming a long K is latency-bound: each CU moves only the bytes
   // it keeps in flight, and the register path keeps two more K stages in flight than the direct
   // copies (measured on MI355X, 4096 x 512 x 2048: 22.3 -> 15.8 us).  On grids of several tiles
