@@ -62,11 +62,28 @@ int tt_device_count(void);
  *   0 norm1.weight[D]  1 norm1.bias[D]  2 Wqkv[3D,D] (q rows, k rows, v rows)  3 bqkv[3D]
  *   4 out_proj.weight[D,D]  5 out_proj.bias[D]  6 norm2.weight[D]  7 norm2.bias[D]
  *   8 ffn_in.weight[F,D]  9 ffn_in.bias[F]  10 ffn_out.weight[D,F]  11 ffn_out.bias[D]
- * then final_norm.weight[D], final_norm.bias[D] after the last layer.
- * Writes the 12 per-layer segment offsets (elements, relative to the layer start), the layer
- * stride, the final-norm offset and the total element count. */
-int tt_weight_layout(int d_model, int ffn_dim, int num_layers, int64_t layer_offsets[12],
-                     int64_t* layer_stride, int64_t* final_norm_offset, int64_t* total_elems);
+ * and six segments derived from those by tt_pack_derived (the LayerNorms folded into the
+ * projections that follow them):
+ *   12 Wqkv'[3D,D] = Wqkv diag(norm1.weight)  13 cqkv[3D] fp32 = row sums of Wqkv'
+ *   14 bqkv'[3D] fp32 = bqkv + Wqkv norm1.bias  15 W1'[F,D] = ffn_in.weight diag(norm2.weight)
+ *   16 c1[F] fp32 = row sums of W1'  17 b1'[F] fp32 = ffn_in.bias + ffn_in.weight norm2.bias
+ * (fp32 segments hold two fp16 slots per value), then final_norm.weight[D], final_norm.bias[D]
+ * after the last layer.  Writes the TT_LAYER_SEGMENTS per-layer segment offsets (elements,
+ * relative to the layer start), the layer stride, the final-norm offset and the total element
+ * count. */
+#define TT_LAYER_SEGMENTS 18
+int tt_weight_layout(int d_model, int ffn_dim, int num_layers,
+                     int64_t layer_offsets[TT_LAYER_SEGMENTS], int64_t* layer_stride,
+                     int64_t* final_norm_offset, int64_t* total_elems);
+
+/* Fill segments 12-17 of every layer of a packed weight buffer from its segments 0-11 (one kernel
+ * launch on `stream`; call after the base segments are written and whenever they change).  With
+ * LayerNorm y = (x - mean) rstd gamma + beta, LN(x) W^T + b = rstd (x W'^T - mean c) + b': the
+ * layer-wise plan then multiplies the raw residual stream by W' and applies the per-row
+ * statistics in the GEMM epilogue instead of launching a LayerNorm.  No counterpart in the
+ * reference, which launches residual_layer_norm (kernels/case8_fusions.py:82-221) or fuses the
+ * norm into its Triton tiles (kernels/case13_linear.py:179-259). */
+int tt_pack_derived(void* weights, int d_model, int ffn_dim, int num_layers, void* stream);
 
 /* Execution plans of tt_transformer_fwd. */
 #define TT_PLAN_AUTO 0       /* fused-LN layer-wise plan for d_model <= 128 and at most 2048

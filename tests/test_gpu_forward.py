@@ -167,3 +167,106 @@ def test_stage_parity_layer0(device):
         assert err <= tol, (name, err)
     assert (x2.cpu()[~v].view(torch.int16) == 0).all()
     del hd
+
+
+# ---------------------------------------------------------------- folded LayerNorm
+def test_pack_derived_segments(device):
+    """Segments 12-17 written by tt_pack_derived: W' = fp16(W * gamma) exactly, c = row sums of
+    W' and b' = b + W beta (fp32, against float64 sums of the same fp16 values)."""
+    from tttj_2026_amd import _lib
+    from tttj_2026_amd.optimized_transformer import pack_model_weights
+
+    cfg = TransformerConfig(1, 8, 128, 4, 320, 2, True)
+    model = build_model(cfg, seed=31)
+    g = torch.Generator().manual_seed(32)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if "norm" in name:
+                p.add_(0.3 * torch.randn(p.shape, generator=g))
+    gm = model.half().to(device)
+    packed = pack_model_weights(gm)
+    torch.cuda.synchronize()
+    offs, stride, _, _ = _lib.weight_layout(128, 320, 2)
+    P = packed.cpu()
+    D, F = 128, 320
+    for l in range(2):
+        base = l * stride
+        seg = lambda i, n: P[base + offs[i]: base + offs[i] + n]
+        fp32 = lambda i, n: seg(i, 2 * n).view(torch.float32)
+        for (w_i, g_i, b_i, bias_i, wp_i, c_i, bp_i, rows) in (
+                (2, 0, 1, 3, 12, 13, 14, 3 * D), (8, 6, 7, 9, 15, 16, 17, F)):
+            W = seg(w_i, rows * D).view(rows, D)
+            gam, bet, bias = seg(g_i, D), seg(b_i, D), seg(bias_i, rows)
+            Wp = seg(wp_i, rows * D).view(rows, D)
+            assert torch.equal(Wp, (W.float() * gam.float()).half())
+            c_ref = Wp.double().sum(1)
+            b_ref = bias.double() + (W.double() * bet.double()).sum(1)
+            assert torch.allclose(fp32(c_i, rows).double(), c_ref, atol=1e-4, rtol=1e-5)
+            assert torch.allclose(fp32(bp_i, rows).double(), b_ref, atol=1e-4, rtol=1e-5)
+
+
+@pytest.mark.parametrize("shape", [(2, 64, 256, 4, 1024, 3, False, False),
+                                   (3, 100, 512, 8, 2048, 2, True, True),
+                                   (1, 32, 96, 3, 160, 2, True, False)],
+                         ids=["D256", "D512-masked", "D96-small-kernel"])
+def test_folded_layernorm_large_input_perturbed_norms(device, shape):
+    """The folded LayerNorm (statistics from the producer's partial slots, W' and the epilogue
+    correction) at input scale 30 with non-default LayerNorm parameters: the gate still holds,
+    so the single-pass partial statistics and the rstd (acc - mean c) form do not cancel badly."""
+    b, s, d, h, f, l, causal, masked = shape
+    cfg = TransformerConfig(b, s, d, h, f, l, causal)
+    model = build_model(cfg, seed=41)
+    x16, mask = make_inputs(cfg, masked, 42, min_valid=max(1, s // 2))
+    x16 = (x16.float() * 30.0).half()
+    print(f"[fold] {shape}", flush=True)
+    res, _, _, _ = _run(model, x16, mask if masked else None, device, perturb_ln=True)
+    print(f"[fold] {shape} {res}", flush=True)
+    assert res["passed"], res
+    assert res["repeat_identical"]
+
+
+def test_every_tile_perturbed_norms(device):
+    """Every GEMM tile configuration forced in turn (with tile 5, the narrow kernel, the
+    LayerNorms are folded and its statistics slots are 32 columns wide): each forward passes the
+    gate with perturbed LayerNorm parameters."""
+    from tttj_2026_amd import _lib
+
+    lib = _lib.load()
+    cfg = TransformerConfig(2, 128, 512, 8, 1024, 2, True)
+    model = build_model(cfg, seed=51)
+    g = torch.Generator().manual_seed(53)
+    with torch.no_grad():  # perturbed once (_run's perturb_ln would accumulate over the loop)
+        for name, p in model.named_parameters():
+            if "norm" in name:
+                p.add_(0.25 * torch.randn(p.shape, generator=g))
+    x16, mask = make_inputs(cfg, True, 52, min_valid=64)
+    try:
+        for tile in range(10):
+            assert lib.tt_gemm_tile_override(tile) == 0
+            res, _, _, _ = _run(model, x16, mask, device)
+            print(f"[fold] tile {tile} {res}", flush=True)
+            assert res["passed"], (tile, res)
+    finally:
+        lib.tt_gemm_tile_override(-1)
+
+
+@pytest.mark.parametrize("name", ["C1", "C2"])
+def test_folded_layernorm_matches_fused_ln_plan(device, name):
+    """At the few-token workloads the layer-wise plan folds the LayerNorms; its output agrees
+    with the fused-LN plan (LayerNorm computed in LDS from the unfolded weights) far inside the
+    gate, with perturbed LayerNorm parameters."""
+    from tttj_2026_amd import PLAN_FUSED_LN
+
+    w = WORKLOADS[name]
+    model = build_model(w.config, seed=61)
+    g = torch.Generator().manual_seed(62)
+    with torch.no_grad():
+        for pname, p in model.named_parameters():
+            if "norm" in pname:
+                p.add_(0.25 * torch.randn(p.shape, generator=g))
+    x16, mask = workload_inputs(name)
+    res_a, _, ya, ref = _run(model, x16, mask, device, plan=PLAN_LAYERWISE)
+    res_b, _, yb, _ = _run(model, x16, mask, device, plan=PLAN_FUSED_LN)
+    print(f"[fold] {name} layerwise {res_a} fused_ln {res_b}", flush=True)
+    assert res_a["passed"] and res_b["passed"]
+    assert (ya.float() - yb.float()).abs().max().item() <= 1e-2

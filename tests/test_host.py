@@ -46,7 +46,9 @@ def test_weight_layout_matches_definition():
         cfg = WORKLOADS[name].config
         d, f, n = cfg.d_model, cfg.ffn_dim, cfg.num_layers
         offs, stride, final, total = _lib.weight_layout(d, f, n)
-        sizes = [d, d, 3 * d * d, 3 * d, d * d, d, d, d, f * d, f, d * f, d]
+        sizes = [d, d, 3 * d * d, 3 * d, d * d, d, d, d, f * d, f, d * f, d,
+                 3 * d * d, 6 * d, 6 * d, f * d, 2 * f, 2 * f]
+        assert len(offs) == len(sizes) == _lib.LAYER_SEGMENTS
         al = lambda v: (v + 63) // 64 * 64
         o = 0
         for i, s in enumerate(sizes):
@@ -60,7 +62,10 @@ def test_workspace_bytes_monotone_and_validated():
     big = _lib.workspace_bytes(2, 4096, 1024, 16, 4096)
     assert 0 < small < big
     # C5 workspace: x, LN/ctx, Q, K, V^T, FFN hidden (fp16) ~ 144 MiB
-    assert big == pytest.approx((4 * 8192 * 1024 + 2 * 1024 * 4096 + 8192 * 4096) * 2, rel=1e-3)
+    # activations (x', LN / context, Q, K, V^T, hidden) + partial LayerNorm statistics
+    # (D / 4 float2 slots per token)
+    assert big == pytest.approx((4 * 8192 * 1024 + 2 * 1024 * 4096 + 8192 * 4096) * 2
+                                + 8192 * (1024 // 4) * 8, rel=1e-3)
     with pytest.raises(ValueError):
         _lib.workspace_bytes(1, 64, 240, 5, 1024)  # head_dim 48
     with pytest.raises(ValueError):  # the megakernel's attention tasks take head_dim 32 / 64

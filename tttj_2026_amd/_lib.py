@@ -41,6 +41,7 @@ SIGNATURES = {
     "tt_layernorm_fwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _P]),
     "tt_linear_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "tt_gemm_tile_override": (_I, [_I]),
+    "tt_pack_derived": (_I, [_P, _I, _I, _I, _P]),
     "tt_mask_info": (_I, [_P, _P, _I, _I, _P]),
     "tt_attention_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "tt_transformer_fwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
@@ -88,10 +89,14 @@ def check(rc: int, what: str) -> None:
     raise RuntimeError(msg)
 
 
+LAYER_SEGMENTS = 18
+
+
 def weight_layout(d_model: int, ffn_dim: int, num_layers: int):
-    """Return (12 per-layer offsets, layer stride, final-norm offset, total elements)."""
+    """Return (LAYER_SEGMENTS per-layer offsets, layer stride, final-norm offset, total
+    elements)."""
     lib = load()
-    offs = (_I64 * 12)()
+    offs = (_I64 * LAYER_SEGMENTS)()
     stride, final, total = _I64(), _I64(), _I64()
     check(lib.tt_weight_layout(d_model, ffn_dim, num_layers, offs, ctypes.byref(stride),
                                ctypes.byref(final), ctypes.byref(total)), "tt_weight_layout")

@@ -116,6 +116,90 @@ __device__ __forceinline__ float seg_sum(float v) {
 
 __device__ __forceinline__ float wave_sum(float v) { return seg_sum<64>(v); }
 
+// Sum over aligned groups of G lanes for G in {4, 8, 16, 32, 64} (quad_perm for 4).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (G == 1) {
+    return v;
+  } else if constexpr (G == 4) {
+    v += dpp_mov<0xB1>(v);  // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);  // quad_perm [2,3,0,1]
+    return v;
+  } else {
+    return seg_sum<G>(v);
+  }
+}
+
+// Partial row statistics for a LayerNorm folded into the next projection: a slot holds
+// (mean, M2) -- the mean and the centred sum of squares -- of N consecutive values of a row.
+// `v` are this lane's NV values; the slot spans the G aligned lanes of the group (NV G values).
+template <int G, int NV>
+__device__ __forceinline__ float2 slot_stats(const float (&v)[NV]) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < NV; ++e) s += v[e];
+  const float mean = group_sum<G>(s) * (1.0f / (NV * G));
+  float q = 0.f;
+#pragma unroll
+  for (int e = 0; e < NV; ++e) {
+    const float t = v[e] - mean;
+    q = fmaf(t, t, q);
+  }
+  return make_float2(mean, group_sum<G>(q));
+}
+
+// combine_row_stats for a row shared by G aligned lanes: lane j takes slots j, j + G, ... (one load
+// each when slots <= G), and the G partial results are merged with group sums.
+template <int G>
+__device__ __forceinline__ float2 combine_row_stats_group(const float2* part, int slots, int K) {
+  const int j = threadIdx.x & (G - 1);
+  const float n = (float)(K / slots);
+  float mean = 0.f, m2 = 0.f, cnt = 0.f;
+  for (int s = j; s < slots; s += G) {
+    const float2 v = part[s];
+    const float tot = cnt + n, d = v.x - mean;
+    m2 += v.y + d * d * (cnt * n / tot);
+    mean += d * (n / tot);
+    cnt = tot;
+  }
+  const float mu = group_sum<G>(cnt * mean) / (float)K;
+  const float d = mean - mu;
+  const float M2 = group_sum<G>(fmaf(cnt * d, d, m2));
+  return make_float2(mu, rsqrtf(M2 / (float)K + 1e-5f));
+}
+
+// (mean, rstd) of a row of K values from its `slots` partial (mean, M2) slots of K / slots values
+// each, biased variance and eps 1e-5 (the statistics nn.LayerNorm uses).  Slots are loaded 16 at a
+// time with one wait (indices clamped, so every load is unconditional), each chunk combined as
+// M2 = sum M2_s + n sum (mean_s - mean)^2, and chunks merged pairwise (Chan et al.).
+__device__ __forceinline__ float2 combine_row_stats(const float2* part, int slots, int K) {
+  constexpr int C = 16;
+  const float n = (float)(K / slots);
+  float mean = 0.f, m2 = 0.f, cnt = 0.f;
+  for (int s0 = 0; s0 < slots; s0 += C) {
+    float2 v[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) v[i] = part[min(s0 + i, slots - 1)];
+    const int c = min(C, slots - s0);
+    float cm = 0.f;
+#pragma unroll
+    for (int i = 0; i < C; ++i) cm += i < c ? v[i].x : 0.f;
+    cm *= __builtin_amdgcn_rcpf((float)c);
+    float cq = 0.f;
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+      const float d = v[i].x - cm;
+      cq += i < c ? fmaf(n * d, d, v[i].y) : 0.f;
+    }
+    const float cn = n * (float)c, tot = cnt + cn;
+    const float d = cm - mean;
+    m2 += cq + d * d * (cnt * cn / tot);
+    mean += d * (cn / tot);
+    cnt = tot;
+  }
+  return make_float2(mean, rsqrtf(m2 / (float)K + 1e-5f));
+}
+
 __device__ __forceinline__ float gelu_erf(float v) {
   // Exact-erf GELU, F.gelu(approximate="none"): v * Phi(v), Phi(v) = erfc(-v / sqrt 2) / 2.
   // With z = |v| / sqrt 2, erfc(z) = t * exp(-z^2 + P(t)), t = 1 / (1 + z/2) and P a degree-9

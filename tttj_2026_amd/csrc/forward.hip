@@ -35,15 +35,19 @@ static int64_t align64(int64_t v) { return (v + 63) / 64 * 64; }
 static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
 struct Layout {
-  int64_t off[12];
+  int64_t off[TT_LAYER_SEGMENTS];
   int64_t stride, final_off, total;
 };
 
+// Segments 12-17 are derived from 0-11 (tt_pack_derived): the QKV and ffn_in weights with the
+// LayerNorm gain folded in, W' = W diag(gamma) (fp16), their row sums c = sum_k W'[n, k] and the
+// folded biases b' = b + W beta (both fp32, two halfs per value).
 static Layout weight_layout(int64_t D, int64_t F, int64_t L) {
-  const int64_t sizes[12] = {D, D, 3 * D * D, 3 * D, D * D, D, D, D, F * D, F, D * F, D};
+  const int64_t sizes[TT_LAYER_SEGMENTS] = {D, D, 3 * D * D, 3 * D, D * D, D, D, D, F * D, F, D * F,
+                                            D, 3 * D * D, 6 * D, 6 * D, F * D, 2 * F, 2 * F};
   Layout lay{};
   int64_t o = 0;
-  for (int i = 0; i < 12; ++i) {
+  for (int i = 0; i < TT_LAYER_SEGMENTS; ++i) {
     lay.off[i] = o;
     o += align64(sizes[i]);
   }
@@ -55,6 +59,7 @@ static Layout weight_layout(int64_t D, int64_t F, int64_t L) {
 
 struct Workspace {
   half *xa, *xn, *qkv, *hbuf;
+  float2* part;   // partial row statistics of the residual stream, D / 4 slots per row at most
   int32_t* info;
   size_t bytes;
 };
@@ -69,9 +74,10 @@ static Workspace carve(char* base, int64_t B, int64_t S, int64_t D, int64_t F) {
     return p;
   };
   w.xa = (half*)take(T * D * 2);
-  w.xn = (half*)take(T * D * 2);  // LN output, then attention context, then LN2 output
+  w.xn = (half*)take(T * D * 2);  // LN1 output of layer 0, then the attention context
   w.qkv = (half*)take((2 * T * D + B * D * Sp) * 2);
   w.hbuf = (half*)take(T * F * 2);
+  w.part = (float2*)take(T * (D / 4) * sizeof(float2));
   w.info = (int32_t*)take(2 * B * 4);
   w.bytes = o;
   return w;
@@ -104,7 +110,7 @@ extern "C" int tt_device_count(void) {
 }
 
 extern "C" int tt_weight_layout(int d_model, int ffn_dim, int num_layers,
-                                int64_t layer_offsets[12], int64_t* layer_stride,
+                                int64_t layer_offsets[TT_LAYER_SEGMENTS], int64_t* layer_stride,
                                 int64_t* final_norm_offset, int64_t* total_elems) {
   TT_REQUIRE(d_model > 0 && ffn_dim > 0 && num_layers > 0, "weight_layout: bad shape");
   const Layout lay = weight_layout(d_model, ffn_dim, num_layers);
@@ -113,6 +119,15 @@ extern "C" int tt_weight_layout(int d_model, int ffn_dim, int num_layers,
   if (final_norm_offset) *final_norm_offset = lay.final_off;
   if (total_elems) *total_elems = lay.total;
   return TT_OK;
+}
+
+extern "C" int tt_pack_derived(void* weights, int d_model, int ffn_dim, int num_layers,
+                               void* stream) {
+  TT_REQUIRE(weights != nullptr && d_model > 0 && ffn_dim > 0 && num_layers > 0,
+             "pack_derived: bad arguments");
+  const Layout lay = weight_layout(d_model, ffn_dim, num_layers);
+  return launch_pack_derived((half*)weights, lay.stride, lay.off, d_model, ffn_dim, num_layers,
+                             (hipStream_t)stream);
 }
 
 // Token count up to which the automatic plan runs the persistent megakernel.  Measured on MI355X
@@ -248,6 +263,19 @@ int transformer_fwd(const void* weights, const void* x, const uint8_t* mask, voi
   const bool fused_ln = resolve_plan(plan, B, S, D, H, F) == TT_PLAN_FUSED_LN;
   if (fused_ln && ((rc = ln_tile_supported(D, 3 * D)) != TT_OK || (rc = ln_tile_supported(D, F)) != TT_OK))
     return rc;
+  // Layer-wise plan: LN2 of every layer and LN1 of layers >= 1 are folded into the projection
+  // that follows them (lnfold.hip): the producer of the residual stream (out_proj, ffn_out)
+  // writes partial row statistics in its epilogue, and the QKV / ffn_in GEMMs multiply the raw
+  // residual stream by W' = W diag(gamma) and apply rstd (acc - mean c) + b'.  Layer 0's LN1 (the
+  // input has no producer here) and the final norm stay standalone launches.
+  const int ldp = D / 4;     // float2 slots per row of ws.part (the narrowest producer: 4 columns)
+  int part_slots = 0;        // slots per row the last producer wrote
+  // The fold pays only where launches dominate: for few tokens, whose QKV / ffn_in GEMMs run on
+  // the narrow / small kernels (the statistics loads overlap their K loop).  On the MFMA tiles of
+  // larger shapes the epilogue work it adds is exposed and costs more than the LayerNorm launch
+  // it removes (measured on MI355X: C5 +3.9%, C4 +5.5%), so LN1 / LN2 stay standalone there.
+  const bool fold = !fused_ln && linear_is_narrow(T, 3 * D, D, TT_EPI_QKV) &&
+                    linear_is_narrow(T, F, D, TT_EPI_BIAS_GELU);
   const half* cur = (const half*)x;
   for (int l = 0; l < L; ++l) {
     const half* w = wts + (size_t)l * lay.stride;
@@ -269,12 +297,20 @@ int transformer_fwd(const void* weights, const void* x, const uint8_t* mask, voi
       if ((rc = launch_ln_tile(cur, w + lay.off[0], w + lay.off[1], w + lay.off[2], ep, B, S, D,
                                3 * D, stream)) != TT_OK)
         return rc;
-    } else {
+    } else if (l == 0 || !fold) {
       if ((rc = launch_layernorm(cur, w + lay.off[0], w + lay.off[1], mask, ws.xn, T, D, 1e-5f,
                                  stream)) != TT_OK)
         return rc;
       ep.valid = mask;
       if ((rc = launch_linear(ws.xn, w + lay.off[2], T, 3 * D, D, ep, stream)) != TT_OK) return rc;
+    } else {
+      ep.valid = mask;
+      ep.ln_part = ws.part;
+      ep.ln_slots = part_slots;
+      ep.ln_stride = ldp;
+      ep.ln_colsum = (const float*)(w + lay.off[13]);
+      ep.ln_bias = (const float*)(w + lay.off[14]);
+      if ((rc = launch_linear(cur, w + lay.off[12], T, 3 * D, D, ep, stream)) != TT_OK) return rc;
     }
     if ((rc = launch_attention(q, k, vt, mask, info, ws.xn, B, S, H, hd, causal, stream)) != TT_OK)
       return rc;
@@ -286,6 +322,11 @@ int transformer_fwd(const void* weights, const void* x, const uint8_t* mask, voi
     ep.y = ws.xa;
     ep.ldy = D;
     ep.mode = TT_EPI_RESID_MASKED;
+    if (fold) {
+      ep.part_out = ws.part;
+      ep.ln_stride = ldp;
+      part_slots = D / linear_stats_width(T, D, D, TT_EPI_RESID_MASKED);
+    }
     if ((rc = launch_linear(ws.xn, w + lay.off[4], T, D, D, ep, stream)) != TT_OK) return rc;
     ep = EpiArgs{};
     ep.bias = w + lay.off[9];
@@ -296,13 +337,22 @@ int transformer_fwd(const void* weights, const void* x, const uint8_t* mask, voi
       if ((rc = launch_ln_tile(ws.xa, w + lay.off[6], w + lay.off[7], w + lay.off[8], ep, B, S, D,
                                F, stream)) != TT_OK)
         return rc;
-    } else {
+    } else if (!fold) {
       if ((rc = launch_layernorm(ws.xa, w + lay.off[6], w + lay.off[7], mask, ws.xn, T, D, 1e-5f,
                                  stream)) != TT_OK)
         return rc;
       ep.valid = mask;
       ep.seq = S;  // row-tile balancing of padded batches
       if ((rc = launch_linear(ws.xn, w + lay.off[8], T, F, D, ep, stream)) != TT_OK) return rc;
+    } else {
+      ep.valid = mask;
+      ep.seq = S;  // row-tile balancing of padded batches
+      ep.ln_part = ws.part;
+      ep.ln_slots = part_slots;
+      ep.ln_stride = ldp;
+      ep.ln_colsum = (const float*)(w + lay.off[16]);
+      ep.ln_bias = (const float*)(w + lay.off[17]);
+      if ((rc = launch_linear(ws.xa, w + lay.off[15], T, F, D, ep, stream)) != TT_OK) return rc;
     }
     ep = EpiArgs{};
     ep.bias = w + lay.off[11];
@@ -312,6 +362,11 @@ int transformer_fwd(const void* weights, const void* x, const uint8_t* mask, voi
     ep.y = ws.xa;
     ep.ldy = D;
     ep.mode = TT_EPI_MASKED_RESID;
+    if (fold && l + 1 < L) {  // statistics for the next layer's LN1
+      ep.part_out = ws.part;
+      ep.ln_stride = ldp;
+      part_slots = D / linear_stats_width(T, D, F, TT_EPI_MASKED_RESID);
+    }
     if ((rc = launch_linear(ws.hbuf, w + lay.off[10], T, D, F, ep, stream)) != TT_OK) return rc;
     cur = ws.xa;
   }

@@ -202,6 +202,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1)
   __shared__ __align__(16) half sbias[BN];
   if (threadIdx.x < BN / 8)
     *(u32x4*)(sbias + 8 * threadIdx.x) = *(const u32x4*)(ep.bias + n0 + 8 * threadIdx.x);
+  constexpr bool ZERO_MASKED = MODE == TT_EPI_BIAS || MODE == TT_EPI_BIAS_GELU || MODE == TT_EPI_QKV;
 
   // Fragment addressing: A = W rows (output features), B = X rows (tokens); lane l reads row
   // l % 32 of a 32-row block at logical chunk 2 kk + l / 32, physically XOR bits 1-3 of the row
@@ -416,7 +417,6 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1)
   }
   // Modes without a residual write masked rows as +0.0 (the residual modes handle the mask
   // when they store).
-  constexpr bool ZERO_MASKED = MODE == TT_EPI_BIAS || MODE == TT_EPI_BIAS_GELU || MODE == TT_EPI_QKV;
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
     const int ml = j * 32 + (lane & 31);
@@ -533,7 +533,6 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1)
           qk_row += (size_t)(ep.heads - 1) * S * hd;
         }
       }
-      if (m >= M) continue;
       if constexpr (RESID) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -542,7 +541,17 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1)
           else
             t[e] = ok[q] ? (half)((float)rv[q][e] + (float)t[e]) : (half)0.f;
         }
+        if (ep.part_out != nullptr) {
+          // partial (mean, M2) of this row over the wave's WN columns (CPR lanes, aligned):
+          // the statistics of the next LayerNorm, folded into the next projection
+          float f[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = (float)t[e];
+          const float2 st = slot_stats<CPR, 8>(f);
+          if (c == 0 && m < M) ep.part_out[(size_t)m * ep.ln_stride + nw / WN] = st;
+        }
       }
+      if (m >= M) continue;
       half* dst;
       if constexpr (MODE == TT_EPI_QKV) {
         dst = qk_col + row_off;  // Q or K: 8 features of one head of token m
@@ -556,13 +565,41 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1)
 
 // Epilogue of 4 consecutive outputs n .. n + 3 of row m from their fp32 sums (the semantics of
 // gemm_kernel's epilogue, element by element), for the small-shape and narrow-tile kernels.
-template <int MODE>
-__device__ __forceinline__ void epilogue4(const EpiArgs& ep, int m, int n, const float acc[4]) {
+// G lanes (aligned) share a row and hold consecutive 4-column groups of it: with ep.part_out,
+// they write the partial statistics slot of their 4 G columns; with ep.ln_part, K is the row
+// length of the folded LayerNorm.
+// Folded-LayerNorm inputs of one thread's 4 outputs, loaded before the GEMM's K loop so their
+// latency overlaps it: the row's (mean, rstd) and the 4 columns' c and b'.
+struct LnPre {
+  float2 rs;
+  floatx4 c, b;
+};
+
+template <int MODE, int G>
+__device__ __forceinline__ LnPre ln_pre4(const EpiArgs& ep, int m, int n, int K) {
+  LnPre p{};
+  constexpr bool ZERO_MASKED = MODE == TT_EPI_BIAS || MODE == TT_EPI_BIAS_GELU || MODE == TT_EPI_QKV;
+  if (ZERO_MASKED && ep.ln_part != nullptr) {
+    p.rs = combine_row_stats_group<G>(ep.ln_part + (size_t)m * ep.ln_stride, ep.ln_slots, K);
+    p.c = *(const floatx4*)(ep.ln_colsum + n);
+    p.b = *(const floatx4*)(ep.ln_bias + n);
+  }
+  return p;
+}
+
+template <int MODE, int G>
+__device__ __forceinline__ void epilogue4(const EpiArgs& ep, int m, int n, const float acc[4],
+                                          const LnPre& pre) {
   const bool keep = ep.valid == nullptr || ep.valid[m] != 0;
   half4 hv;
+  constexpr bool ZERO_MASKED = MODE == TT_EPI_BIAS || MODE == TT_EPI_BIAS_GELU || MODE == TT_EPI_QKV;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    float v = acc[e] + (float)ep.bias[n + e];
+    float v;
+    if (ZERO_MASKED && ep.ln_part != nullptr)
+      v = fmaf(pre.rs.y, fmaf(-pre.rs.x, pre.c[e], acc[e]), pre.b[e]);
+    else
+      v = acc[e] + (float)ep.bias[n + e];
     if constexpr (MODE == TT_EPI_BIAS_GELU) v = gelu_erf(v);
     hv[e] = (half)v;
   }
@@ -592,6 +629,13 @@ __device__ __forceinline__ void epilogue4(const EpiArgs& ep, int m, int n, const
         else
           hv[e] = keep ? (half)((float)rv[e] + (float)hv[e]) : (half)0.f;
       }
+      if (ep.part_out != nullptr) {
+        float f[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[e] = (float)hv[e];
+        const float2 st = slot_stats<G, 4>(f);
+        if ((threadIdx.x & (G - 1)) == 0) ep.part_out[(size_t)m * ep.ln_stride + n / (4 * G)] = st;
+      }
     } else if (!keep) {
       hv = half4{(half)0.f, (half)0.f, (half)0.f, (half)0.f};
     }
@@ -611,6 +655,7 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const half* __restrict_
   const long g = (long)blockIdx.x * 256 + threadIdx.x;
   if (g >= (long)M * ngroups) return;
   const int m = (int)(g / ngroups), n = (int)(g - (long)m * ngroups) * 4;
+  const LnPre pre = ln_pre4<MODE, 1>(ep, m, n, K);
   const half* xr = X + (size_t)m * K;
   const half* wr = W + (size_t)n * K;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -623,7 +668,7 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const half* __restrict_
       for (int t = 0; t < 8; ++t) acc[e] = fmaf((float)xv[t], (float)wv[t], acc[e]);
     }
   }
-  epilogue4<MODE>(ep, m, n, acc);
+  epilogue4<MODE, 1>(ep, m, n, acc, pre);
 }
 
 static int run_small(int mode, const half* x, const half* w, int m, int n, int k,
@@ -673,6 +718,9 @@ __global__ __launch_bounds__(256) void gemm_narrow_kernel(const half* __restrict
   const half* wr = W + (size_t)(n0 + r) * K + kh;
   const int steps = K / 16 / 4;          // K steps of this wave (K % 64 == 0)
   const int kbeg = wave * steps * 16;
+  // epilogue mapping (below): thread -> row ml, 4 columns nl; 8 aligned threads per row
+  const int ml = threadIdx.x >> 3, nl = 4 * (threadIdx.x & 7);
+  const LnPre pre = ln_pre4<MODE, 8>(ep, min(m0 + ml, M - 1), n0 + nl, K);
   floatx16 acc;
 #pragma unroll
   for (int e = 0; e < 16; ++e) acc[e] = 0.f;
@@ -706,13 +754,12 @@ __global__ __launch_bounds__(256) void gemm_narrow_kernel(const half* __restrict
     *(floatx4*)&part[wave][r][8 * g + 4 * (lane >> 5)] =
         floatx4{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
   __syncthreads();
-  const int ml = threadIdx.x >> 3, nl = 4 * (threadIdx.x & 7);
   if (m0 + ml >= M) return;
   float sum[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e)
     sum[e] = ((part[0][ml][nl + e] + part[1][ml][nl + e]) + part[2][ml][nl + e]) + part[3][ml][nl + e];
-  epilogue4<MODE>(ep, m0 + ml, n0 + nl, sum);
+  epilogue4<MODE, 8>(ep, m0 + ml, n0 + nl, sum, pre);
 }
 
 static int run_narrow(int mode, const half* x, const half* w, int m, int n, int k,
@@ -829,6 +876,18 @@ static int device_cus() {
   return cus;
 }
 
+bool linear_is_narrow(int m, int n, int k, int mode) {
+  if (k % kBK != 0 || n % 64 != 0) return true;
+  return pick_tile(m, n, k, mode, device_cus()) == 5;
+}
+
+int linear_stats_width(int m, int n, int k, int mode) {
+  if (k % kBK != 0 || n % 64 != 0) return 4;  // gemm_small_kernel: one thread per 4 columns
+  const int tile = pick_tile(m, n, k, mode, device_cus());
+  if (tile == 5) return kNarrow;               // gemm_narrow_kernel: 8 threads per 32 columns
+  return kTiles[tile].bn / 2;                  // MFMA tiles: the column range of one wave
+}
+
 int launch_linear(const half* x, const half* w, int m, int n, int k, const EpiArgs& ep,
                   hipStream_t stream) {
   TT_REQUIRE(m >= 0 && n > 0 && k > 0, "linear: bad shape m=%d n=%d k=%d", m, n, k);
@@ -849,6 +908,23 @@ int launch_linear(const half* x, const half* w, int m, int n, int k, const EpiAr
                    (long)ep.batch * ep.seq == m,
                "linear(qkv): inconsistent shape m=%d n=%d batch=%d seq=%d heads=%d hd=%d", m, n,
                ep.batch, ep.seq, ep.heads, ep.head_dim);
+  }
+  if (ep.ln_part != nullptr) {
+    TT_REQUIRE(ep.mode == TT_EPI_QKV || ep.mode == TT_EPI_BIAS_GELU || ep.mode == TT_EPI_BIAS,
+               "linear: a folded LayerNorm needs a bias / GELU / QKV epilogue");
+    TT_REQUIRE(linear_is_narrow(m, n, k, ep.mode),
+               "linear: a folded LayerNorm runs on the narrow / small kernels only (m=%d n=%d)", m, n);
+    TT_REQUIRE(ep.ln_colsum != nullptr && ep.ln_bias != nullptr && ep.ln_slots > 0 &&
+                   k % ep.ln_slots == 0 && ep.ln_stride >= ep.ln_slots,
+               "linear: bad folded-LayerNorm arguments (slots %d, stride %d, K %d)", ep.ln_slots,
+               ep.ln_stride, k);
+  }
+  if (ep.part_out != nullptr) {
+    TT_REQUIRE(ep.mode == TT_EPI_RESID_MASKED || ep.mode == TT_EPI_MASKED_RESID,
+               "linear: row statistics are written by the residual epilogues only");
+    TT_REQUIRE(ep.ln_stride >= n / linear_stats_width(m, n, k, ep.mode),
+               "linear: statistics row stride %d < %d slots", ep.ln_stride,
+               n / linear_stats_width(m, n, k, ep.mode));
   }
   if (m == 0) return TT_OK;
   if (k % kBK != 0 || n % 64 != 0) return run_small(ep.mode, x, w, m, n, k, ep, stream);

@@ -13,6 +13,18 @@ struct EpiArgs {
   int ldy;
   int mode;              // TT_EPI_*
   int batch, seq, heads, head_dim, d_model;  // TT_EPI_QKV only
+  // LayerNorm folded into this projection (TT_EPI_QKV / TT_EPI_BIAS_GELU, on the narrow and
+  // small kernels): X is the raw residual stream, W = W diag(gamma), and the epilogue computes
+  // rstd (acc - mean c) + b' instead of acc + bias.  The row statistics come from ln_slots
+  // partial (mean, M2) slots per row (row stride ln_stride float2), each over K / ln_slots
+  // columns.
+  const float2* ln_part;  // [M][ln_stride] or nullptr
+  const float* ln_colsum; // c [N]
+  const float* ln_bias;   // b' [N]
+  int ln_slots, ln_stride;
+  // Producer side (residual modes): partial (mean, M2) slots of the values written, one per
+  // stats_width columns (stats_width = linear_stats_width(...)), row stride ln_stride.
+  float2* part_out;       // [M][ln_stride] or nullptr
 };
 
 int launch_layernorm(const half* x, const half* gamma, const half* beta, const uint8_t* valid,
@@ -20,6 +32,15 @@ int launch_layernorm(const half* x, const half* gamma, const half* beta, const u
 
 int launch_linear(const half* x, const half* w, int m, int n, int k, const EpiArgs& ep,
                   hipStream_t stream);
+// Columns per partial-statistics slot the GEMM launch_linear would run for this shape writes
+// (the column range of one wave, or of one thread group on the narrow and small kernels).
+int linear_stats_width(int m, int n, int k, int mode);
+// Whether launch_linear runs this shape on the narrow (32 x 32) or small (vector-ALU) kernel.
+bool linear_is_narrow(int m, int n, int k, int mode);
+
+// Derived segments 12-17 of the packed weights (lnfold.hip).
+int launch_pack_derived(half* w, int64_t stride, const int64_t* off, int D, int F, int L,
+                        hipStream_t stream);
 
 int launch_mask_info(const uint8_t* mask, int32_t* info, int batch, int seq, hipStream_t stream);
 

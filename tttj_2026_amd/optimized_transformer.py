@@ -100,7 +100,9 @@ def pack_model_weights(model: nn.Module) -> torch.Tensor:
 
     Generalises kernels/sequence_resident.py:74-109 (F == D only) to any F; q, k and v weights and
     biases are concatenated into one [3D, D] projection.  Segment offsets come from the library
-    (``tt_weight_layout``) so Python and C cannot disagree about the layout.
+    (``tt_weight_layout``) so Python and C cannot disagree about the layout; the derived segments
+    (LayerNorm gains and biases folded into the QKV and ffn_in weights) are computed on the device
+    by ``tt_pack_derived``.
     """
     cfg = model.config
     d, f, n_layers = cfg.d_model, cfg.ffn_dim, cfg.num_layers
@@ -140,6 +142,11 @@ def pack_model_weights(model: nn.Module) -> torch.Tensor:
     dpad = (d + 63) // 64 * 64
     packed[final:final + d].copy_(model.final_norm.weight.detach().reshape(-1))
     packed[final + dpad:final + dpad + d].copy_(model.final_norm.bias.detach().reshape(-1))
+    # segments 12-17: the LayerNorms folded into the projections that follow them
+    lib = _lib.load()
+    _lib.check(lib.tt_pack_derived(packed.data_ptr(), d, f, n_layers,
+                                   torch.cuda.current_stream(packed.device).cuda_stream),
+               "tt_pack_derived")
     return packed
 
 
