@@ -61,7 +61,8 @@ int launch_attention_small(const AttnArgs& args, const int32_t* info, int head_d
 // its first use and then reused unchanged between launches of the same shape.
 size_t megakernel_workspace_bytes(int B, int S, int D, int F, int L);
 int megakernel_supported(int B, int S, int D, int H, int F, int L);
-int launch_megakernel(const half* weights, const int64_t off[12], int64_t stride, int64_t final_off,
+int launch_megakernel(const half* weights, const int64_t off[TT_LAYER_SEGMENTS], int64_t stride,
+                      int64_t final_off,
                       const half* x, const uint8_t* mask, half* y, char* workspace,
                       int64_t workspace_bytes, int B, int S, int D, int H, int F, int L, int causal,
                       uint64_t* trace, hipStream_t stream);

@@ -2,16 +2,19 @@
 // with a workgroup-level dependency DAG in place of the per-op launches of the layer-wise plan.
 //
 // Tasks (row block rb = 64 consecutive tokens of one sequence; query block qb = 128 tokens):
-//   QKV(l, rb, nt)   LN1_l of the rows of rb (from x for l = 0, else the residual stream xa) is
-//                    computed straight into LDS, then 64 columns of [Q | K | V^T]
+//   QKV(l, rb, nt)   64 columns of [Q | K | V^T] = LN1_l(X[rb]) Wqkv^T + b for X = x (l = 0) or
+//                    the residual stream xa, with the LayerNorm folded into the weights
+//                    (W' = W diag(gamma), epilogue rstd (acc - mean c) + b'); the rows' statistics
+//                    are computed from the A operand as it streams through LDS
 //   ATT(l, b, h, qb) attention of query block qb of sequence b, head h -> ctx
 //   OUT(l, rb, nt)   xa[rb, nt] = resid + mask(ctx Wo^T + bo)
-//   FF1(l, rb, nt)   LN2_l of the rows of rb into LDS, then h[rb, nt] = GELU(LN2 W1^T + b1)
-//   FF2(l, rb, nt)   xa[rb, nt] = mask(xa + h W2^T + b2)
+//   FF1(l, rb, nt)   h[rb, nt] = GELU(LN2(xa[rb]) W1^T + b1), LayerNorm folded as in QKV
+//   FF2(l, rb, nt, s) split s of K = ffn_dim of xa[rb, nt] = mask(xa + h W2^T + b2): each split
+//                    stores an fp32 partial and the last one to arrive sums them in split order
+//                    and runs the epilogue
 //   FIN(rb)          y[rb] = mask(final_norm(xa[rb]))
-// A task computing LayerNorm reads complete rows written by other tasks, so it waits for all of
-// them; recomputing the norm in each of its consumers (instead of one task writing it out) keeps
-// it off the critical path and saves a global round trip.
+// No task waits for a LayerNorm: the norms of QKV / FF1 ride on the GEMM's own A stream.  An FF2
+// split waits only for the FF1 tiles of its K range.
 // Tasks are numbered in a topological order and handed out statically (task t to workgroup
 // t mod G).  Every task waits only on tasks numbered before it, and all G workgroups are
 // resident at once, so the smallest unfinished task can always run: the DAG cannot deadlock.
@@ -64,23 +67,31 @@ constexpr int kRingW = 8;                   // K steps in flight (weights only)
 constexpr int kRingAW = kLdsHalfs / kStepAW;  // = 9
 static_assert(kResA + kRingW * kStepW <= kLdsHalfs && kRingAW * kStepAW <= kLdsHalfs, "LDS map");
 
-enum Counter : int { cQKV = 0, cATT, cOUT, cFF1, cFF2, kNumCounters };
+// Dependency counters, kSub per (layer, kind, row block): QKV, ATT, OUT and FF2 (tiles of a row
+// block whose output is complete) use sub-counter 0; FF1 counts finished tiles per FF2 split
+// (sub = split); FF2T counts the arrivals of the splits of FF2 tile nt (sub = nt).
+enum Counter : int { cQKV = 0, cATT, cOUT, cFF1, cFF2, cFF2T, kNumCounters };
+constexpr int kSub = 8;            // >= FF2 splits and >= d_model / 64 (d_model <= kMaxD)
+static_assert(kSub * kNB >= kMaxD, "one FF2T sub-counter per output tile of a row block");
+constexpr int kMinSplitSteps = 4;  // K steps (of 64) per FF2 split at least
 
 struct MegaParams {
   const half* w;
-  int64_t off[12];
+  int64_t off[TT_LAYER_SEGMENTS];
   int64_t stride, final_off;
   const half* x;
   half* y;
   const uint8_t* mask;
   half *xa, *ctx, *q, *k, *vt, *hbuf;
-  uint32_t* cnt;    // [L * kNumCounters * nrb]
+  float* part;      // FF2 split partials: [nrb][td][ks][256 lanes x 16] fp32
+  uint32_t* cnt;    // [L][kNumCounters][nrb][kSub]
   uint32_t* ctrl;   // [0] epoch, [1] finished workgroups, [2] error flag, [4..5] host mirror
                     // address of the error flag (0: none), set by megakernel_attach_status
   uint64_t* trace;  // optional: 4 words per task (task | wg << 32, start, ready, end) or nullptr
   uint32_t spin_limit;  // polls per dependency wait before it gives up (kSpinLimit by default)
   int B, S, D, H, F, L, causal;
   int nsb, nqb, nrb, tq, td, tf;  // row / query blocks per sequence, row blocks, N tiles
+  int ks, ksteps;                 // FF2 splits of K = ffn_dim, K steps (of 64) per split
   int per_layer, ntask;
   float scale_log2;
 };
@@ -99,8 +110,9 @@ __device__ __forceinline__ void trace_stamp(const MegaParams& p, int task, int s
   }
 }
 
-__device__ __forceinline__ uint32_t* counter(const MegaParams& p, int layer, int kind, int rb) {
-  return p.cnt + ((size_t)layer * kNumCounters + kind) * p.nrb + rb;
+__device__ __forceinline__ uint32_t* counter(const MegaParams& p, int layer, int kind, int rb,
+                                             int sub = 0) {
+  return p.cnt + (((size_t)layer * kNumCounters + kind) * p.nrb + rb) * kSub + sub;
 }
 
 // Block-wide: wait until *c has reached `target` (mod 2^32), bounded.  Thread 0 polls and then
@@ -234,24 +246,25 @@ __device__ void mk_layernorm(const half* src, const half* gamma, const half* bet
 // ---- 64 x 64 GEMM tile, K streamed through an LDS ring of K steps ----
 // A K step holds [64 rows][64 halfs] per operand with 16-byte chunks swizzled by row.  Copy i of
 // a wave moves 8 rows (1 KiB): rows 8 (wave + 4 i) + lane / 8, logical chunk (lane % 8) ^ (row % 8).
-__device__ __forceinline__ void mk_copy_w(const half* W, int K, int n0, int k0, half* dst) {
+// `ld` is the operand's row stride and k0 the first column of the step.
+__device__ __forceinline__ void mk_copy_w(const half* W, int ld, int n0, int k0, half* dst) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int r = (wave + 4 * i) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ (lane >> 3);
-    lds_copy16(W + (size_t)(n0 + r) * K + k0 + 8 * c, dst + (wave + 4 * i) * 8 * 64);
+    lds_copy16(W + (size_t)(n0 + r) * ld + k0 + 8 * c, dst + (wave + 4 * i) * 8 * 64);
   }
 }
 
-__device__ __forceinline__ void mk_copy_a(const half* A, int K, int row0, int nrows, int k0,
+__device__ __forceinline__ void mk_copy_a(const half* A, int ld, int row0, int nrows, int k0,
                                           half* dst) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int r = min((wave + 4 * i) * 8 + (lane >> 3), nrows - 1);  // clamped rows: never stored
     const int c = (lane & 7) ^ (lane >> 3);
-    lds_copy16(A + (size_t)(row0 + r) * K + k0 + 8 * c, dst + (wave + 4 * i) * 8 * 64);
+    lds_copy16(A + (size_t)(row0 + r) * ld + k0 + 8 * c, dst + (wave + 4 * i) * 8 * 64);
   }
 }
 
@@ -266,68 +279,86 @@ struct Ring {
   __device__ static half* a(half* lds, int s) { return lds + (s % NS) * kStepAW; }
 };
 
-// Issue the weight copies of the first min(NS - 1, nk) K steps (before the task waits for its
-// inputs: weights never change).
+// Issue the weight copies of the first min(NS - 1, nk) K steps, columns k0 + 64 s (before the
+// task waits for its inputs: weights never change).
 template <bool RESA>
-__device__ __forceinline__ void mk_prefetch_w(const half* W, int K, int n0, half* lds) {
-  const int nk = K / 64;
-  for (int s = 0; s < Ring<RESA>::NS - 1 && s < nk; ++s) mk_copy_w(W, K, n0, s * 64, Ring<RESA>::w(lds, s));
+__device__ __forceinline__ void mk_prefetch_w(const half* W, int ld, int n0, int k0, int nk,
+                                              half* lds) {
+  for (int s = 0; s < Ring<RESA>::NS - 1 && s < nk; ++s)
+    mk_copy_w(W, ld, n0, k0 + s * 64, Ring<RESA>::w(lds, s));
 }
 
-// Y[row0 + m, n0 + n] for the 64 x 64 tile.  A comes from `A` (streamed, RESA == false) or from
-// the resident LayerNorm'd area (RESA == true).  The W copies of the first NS - 1 K steps must
-// have been issued by mk_prefetch_w<RESA>.  Four waves in 2 x 2, each a 32 x 32 MFMA block (W as
-// the A operand, so the accumulator is C^T).
-template <int MODE, bool RESA>
-__device__ void mk_gemm_tile(const half* A, const half* W, int K, int row0, int nrows, int n0,
-                             const EpiArgs& ep, half* lds) {
+// Accumulator of the 64 x 64 tile: sum over K steps s < nk of A[row0 + m][k0 + 64 s ..] .
+// W[n0 + n][k0 + 64 s ..] (row strides lda, ldw).  A comes from `A` (streamed, RESA == false) or from the resident
+// LayerNorm'd area (RESA == true).  The W copies of the first NS - 1 steps must have been issued
+// by mk_prefetch_w<RESA> with the same arguments; loads the caller issues between the two are
+// complete when the first step is.  Four waves in 2 x 2, each a 32 x 32 MFMA block (W as the
+// MFMA's A operand, so the accumulator is C^T): acc[4 g + e] = C[32 wm + lane % 32]
+// [32 wn + 8 g + 4 (lane / 32) + e].
+// STATS (streaming only, the K range being whole rows): also the LayerNorm statistics of the 64 A
+// rows, computed from the K steps as they pass through LDS -- 4 lanes per row take a step's 64
+// values, whose (mean, M2) are merged into the running ones (Chan et al.) -- and left in
+// srow[row] = (mean, rstd), biased variance, eps 1e-5.  The ring is free when this returns.
+template <bool RESA, bool STATS>
+__device__ floatx16 mk_tile_core(const half* A, int lda, const half* W, int ldw, int n0, int k0,
+                                 int nk, int row0, int nrows, half* lds, float2* srow) {
+  static_assert(!(RESA && STATS), "statistics come from the streamed A operand");
   using R = Ring<RESA>;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int frow = lane & 31, fhi = lane >> 5, fx = lane & 7;
-  const int nk = K / 64;
-  constexpr bool RESID = MODE == TT_EPI_RESID_MASKED || MODE == TT_EPI_MASKED_RESID;
-  // Epilogue inputs first (their latency overlaps the main loop): residual and mask of this
-  // lane's row, 4 x 4 features.
-  const int ml = wm * 32 + frow;
-  const int mrow = row0 + min(ml, nrows - 1);
-  half4 res[4], bv[4];
-#pragma unroll
-  for (int g = 0; g < 4; ++g) bv[g] = *(const half4*)(ep.bias + n0 + wn * 32 + 8 * g + 4 * fhi);
-  bool ok = true;
-  if constexpr (RESID) {
-    ok = ep.valid == nullptr || ep.valid[mrow] != 0;
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-      res[g] = *(const half4*)(ep.resid + (size_t)mrow * ep.ldy + n0 + wn * 32 + 8 * g + 4 * fhi);
-  }
+  const int sr = threadIdx.x >> 2, sq = threadIdx.x & 3;  // statistics: row, quarter of a step
   const int pro = min(nk, R::NS - 1);  // K steps whose W copies mk_prefetch_w issued
   if constexpr (!RESA) {
-    for (int s = 0; s < pro; ++s) mk_copy_a(A, K, row0, nrows, s * 64, R::a(lds, s));
+    for (int s = 0; s < pro; ++s) mk_copy_a(A, lda, row0, nrows, k0 + s * 64, R::a(lds, s));
   }
   floatx16 acc;
 #pragma unroll
   for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-  auto step = [&](const half* wb, const half* abase) {
+  float mean = 0.f, m2 = 0.f;
+  auto step = [&](int kt) {
+    const half* wb = R::w(lds, kt);
+    const half* ab = RESA ? lds + kt * kMB * 64 : R::a(lds, kt);
     half8 a[4], b[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int pc = (2 * kk + fhi) ^ fx;
-      b[kk] = *(const half8*)(abase + (wm * 32 + frow) * 64 + pc * 8);
+      b[kk] = *(const half8*)(ab + (wm * 32 + frow) * 64 + pc * 8);
       a[kk] = *(const half8*)(wb + (wn * 32 + frow) * 64 + pc * 8);
+    }
+    half8 u0, u1;
+    if constexpr (STATS) {
+      u0 = *(const half8*)(ab + sr * 64 + (((2 * sq) ^ (sr & 7)) << 3));
+      u1 = *(const half8*)(ab + sr * 64 + (((2 * sq + 1) ^ (sr & 7)) << 3));
     }
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) acc = mfma32x32x16(a[kk], b[kk], acc);
+    if constexpr (STATS) {
+      float v[16];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[e] = (float)u0[e];
+        v[8 + e] = (float)u1[e];
+      }
+      const float2 st = slot_stats<4, 16>(v);  // this step's 64 values of row sr
+      if (kt == 0) {
+        mean = st.x;
+        m2 = st.y;
+      } else {
+        const float n = 64.f * (float)kt, tot = n + 64.f, d = st.x - mean;
+        mean = fmaf(d, 64.f / tot, mean);
+        m2 += fmaf(d * d, n * 64.f / tot, st.y);
+      }
+    }
   };
   if (nk <= R::NS - 1) {
     // Every K step is already in flight: one wait and one barrier.
     wait_vmcnt<0>();
     __syncthreads();
-    for (int kt = 0; kt < nk; ++kt)
-      step(R::w(lds, kt), RESA ? lds + kt * kMB * 64 : R::a(lds, kt));
+    for (int kt = 0; kt < nk; ++kt) step(kt);
   }
   // Issue order of this wave's loads: W copies of the prologue steps (mk_prefetch_w), then the
-  // bias / residual loads, then the A copies of the prologue steps, then W and A of each later
+  // caller's epilogue loads, then the A copies of the prologue steps, then W and A of each later
   // step together.  Step kt is complete once at most the loads issued after its last copy are in
   // flight: `newer` counts those.
   for (int kt = 0; kt < nk && nk > R::NS - 1; ++kt) {
@@ -342,53 +373,165 @@ __device__ void mk_gemm_tile(const half* A, const half* W, int K, int row0, int 
     raw_barrier();
     const int nxt = kt + R::NS - 1;
     if (nxt < nk) {
-      mk_copy_w(W, K, n0, nxt * 64, R::w(lds, nxt));
-      if constexpr (!RESA) mk_copy_a(A, K, row0, nrows, nxt * 64, R::a(lds, nxt));
+      mk_copy_w(W, ldw, n0, k0 + nxt * 64, R::w(lds, nxt));
+      if constexpr (!RESA) mk_copy_a(A, lda, row0, nrows, k0 + nxt * 64, R::a(lds, nxt));
     }
-    step(R::w(lds, kt), RESA ? lds + kt * kMB * 64 : R::a(lds, kt));
+    step(kt);
+  }
+  if constexpr (STATS) {
+    if (sq == 0) srow[sr] = make_float2(mean, rsqrtf(m2 / (float)(64 * nk) + 1e-5f));
   }
   __syncthreads();  // the ring and the resident area are free for the next task
-  // Epilogue straight from registers: acc[4g+e] = C[m][n], m = row0 + 32 wm + lane % 32,
-  // n = n0 + 32 wn + 8 g + 4 (lane / 32) + e.
+  return acc;
+}
+
+// Store 4 consecutive features (row m, columns n .. n + 3) of an epilogue's result: row-major
+// into ep.y, or for TT_EPI_QKV scattered into the Q / K planes ([B, H, S, hd]) and V^T
+// ([B, H, hd, S padded to 64]).
+template <int MODE>
+__device__ __forceinline__ void mk_store4(const EpiArgs& ep, int m, int n, half4 h) {
+  if constexpr (MODE == TT_EPI_QKV) {
+    const int D = ep.d_model, hd = ep.head_dim, S = ep.seq;
+    const int which = n / D, nn = n - which * D;
+    const int hh = nn / hd, d = nn - hh * hd;
+    const int bb = m / S, sq = m - bb * S;
+    const size_t bh = (size_t)bb * ep.heads + hh;
+    const size_t plane = (size_t)ep.batch * S * D;
+    if (which < 2) {
+      *(half4*)(ep.y + which * plane + (bh * S + sq) * hd + d) = h;
+    } else {
+      const size_t ldv = (size_t)(S + 63) / 64 * 64;
+      half* vt = ep.y + 2 * plane + (bh * hd + d) * ldv + sq;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vt[(size_t)e * ldv] = h[e];
+    }
+  } else {
+    *(half4*)(ep.y + (size_t)m * ep.ldy + n) = h;
+  }
+}
+
+// Epilogue operands of this lane's 16 columns and row, loaded before the K loop so that their
+// latency overlaps it: bias; for the residual modes the residual row and its mask bit.
+struct TileCols {
+  half4 bias[4], res[4];
+  bool ok;
+};
+
+// Bias of this lane's 16 columns (a weight: may be loaded before the task's inputs are ready).
+__device__ __forceinline__ void mk_load_bias(TileCols& c, const half* bias, int n0) {
+  const int lane = threadIdx.x & 63, wn = (threadIdx.x >> 6) & 1;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) c.bias[g] = *(const half4*)(bias + n0 + wn * 32 + 8 * g + 4 * (lane >> 5));
+  c.ok = true;
+}
+
+// Residual of this lane's row and 16 columns and the row's mask bit.
+__device__ __forceinline__ void mk_load_resid(TileCols& c, const EpiArgs& ep, int row0, int nrows,
+                                              int n0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int mrow = row0 + min(wm * 32 + (lane & 31), nrows - 1);
+  c.ok = ep.valid == nullptr || ep.valid[mrow] != 0;
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+    c.res[g] = *(const half4*)(ep.resid + (size_t)mrow * ep.ldy + n0 + wn * 32 + 8 * g + 4 * (lane >> 5));
+}
+
+template <int MODE>
+__device__ __forceinline__ TileCols mk_load_cols(const EpiArgs& ep, int row0, int nrows, int n0) {
+  TileCols c;
+  mk_load_bias(c, ep.bias, n0);
+  if constexpr (MODE == TT_EPI_RESID_MASKED || MODE == TT_EPI_MASKED_RESID)
+    mk_load_resid(c, ep, row0, nrows, n0);
+  return c;
+}
+
+// Epilogue straight from registers: bias, then GELU / residual add with the row mask / none,
+// rounded to fp16 and stored (rows past nrows are not stored).
+template <int MODE>
+__device__ void mk_epilogue(const floatx16& acc, const TileCols& c, const EpiArgs& ep, int row0,
+                            int nrows, int n0) {
+  constexpr bool RESID = MODE == TT_EPI_RESID_MASKED || MODE == TT_EPI_MASKED_RESID;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int ml = wm * 32 + (lane & 31);
   if (ml >= nrows) return;
   const int m = row0 + ml;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    const int n = n0 + wn * 32 + 8 * g + 4 * fhi;
+    const int n = n0 + wn * 32 + 8 * g + 4 * (lane >> 5);
     half4 h;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float v = acc[4 * g + e] + (float)bv[g][e];
+      const float v = acc[4 * g + e] + (float)c.bias[g][e];
       if constexpr (MODE == TT_EPI_BIAS_GELU) {
         h[e] = (half)gelu_erf(v);
       } else if constexpr (RESID) {
         const half br = (half)v;  // branch rounded to fp16 first (eager boundary)
-        const half sum = (half)((float)res[g][e] + (float)br);
-        if constexpr (MODE == TT_EPI_RESID_MASKED) h[e] = ok ? sum : res[g][e];
-        else h[e] = ok ? sum : (half)0.f;
+        const half sum = (half)((float)c.res[g][e] + (float)br);
+        if constexpr (MODE == TT_EPI_RESID_MASKED) h[e] = c.ok ? sum : c.res[g][e];
+        else h[e] = c.ok ? sum : (half)0.f;
       } else {
         h[e] = (half)v;
       }
     }
-    if constexpr (MODE == TT_EPI_QKV) {
-      const int D = ep.d_model, hd = ep.head_dim, S = ep.seq;
-      const int which = n / D, nn = n - which * D;
-      const int hh = nn / hd, d = nn - hh * hd;
-      const int bb = m / S, sq = m - bb * S;
-      const size_t bh = (size_t)bb * ep.heads + hh;
-      const size_t plane = (size_t)ep.batch * S * D;
-      if (which < 2) {
-        *(half4*)(ep.y + which * plane + (bh * S + sq) * hd + d) = h;
-      } else {
-        const size_t ldv = (size_t)(S + 63) / 64 * 64;
-        half* vt = ep.y + 2 * plane + (bh * hd + d) * ldv + sq;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) vt[(size_t)e * ldv] = h[e];
-      }
-    } else {
-      *(half4*)(ep.y + (size_t)m * ep.ldy + n) = h;
-    }
+    mk_store4<MODE>(ep, m, n, h);
   }
+}
+
+// Folded-LayerNorm operands of this lane's 16 columns: c = sum_k W'[n][k] with W' = W diag(gamma),
+// and b' = b + W beta (fp32 segments written when the weights are packed).
+struct FoldCols {
+  floatx4 c[4], b[4];
+};
+
+__device__ __forceinline__ FoldCols mk_load_fold(const float* csum, const float* bfold, int n0) {
+  const int lane = threadIdx.x & 63, wn = (threadIdx.x >> 6) & 1;
+  FoldCols f;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int n = n0 + wn * 32 + 8 * g + 4 * (lane >> 5);
+    f.c[g] = *(const floatx4*)(csum + n);
+    f.b[g] = *(const floatx4*)(bfold + n);
+  }
+  return f;
+}
+
+// Epilogue of a projection of LayerNorm(A) computed as A W'^T: per element
+// rstd (acc - mean c) + b', with the row's (mean, rstd) from srow; then GELU (TT_EPI_BIAS_GELU)
+// or the Q / K / V^T scatter (TT_EPI_QKV).
+template <int MODE>
+__device__ void mk_epilogue_fold(const floatx16& acc, const FoldCols& f, const float2* srow,
+                                 const EpiArgs& ep, int row0, int nrows, int n0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int ml = wm * 32 + (lane & 31);
+  if (ml >= nrows) return;
+  const float2 rs = srow[ml];
+  const int m = row0 + ml;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int n = n0 + wn * 32 + 8 * g + 4 * (lane >> 5);
+    half4 h;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v = fmaf(rs.y, fmaf(-rs.x, f.c[g][e], acc[4 * g + e]), f.b[g][e]);
+      if constexpr (MODE == TT_EPI_BIAS_GELU) v = gelu_erf(v);
+      h[e] = (half)v;
+    }
+    mk_store4<MODE>(ep, m, n, h);
+  }
+}
+
+// Y[row0 + m, n0 + n] for the 64 x 64 tile of Y = A W^T + b (K = whole rows), epilogue MODE.
+// The W copies of the first NS - 1 K steps must have been issued by mk_prefetch_w<RESA>.
+template <int MODE, bool RESA>
+__device__ void mk_gemm_tile(const half* A, const half* W, int K, int row0, int nrows, int n0,
+                             const EpiArgs& ep, half* lds) {
+  const TileCols c = mk_load_cols<MODE>(ep, row0, nrows, n0);
+  const floatx16 acc =
+      mk_tile_core<RESA, false>(A, K, W, K, n0, 0, K / 64, row0, nrows, lds, nullptr);
+  mk_epilogue<MODE>(acc, c, ep, row0, nrows, n0);
 }
 
 // kv_end (1 + last valid key) and prefix flag of sequence b, computed by the block.
@@ -449,20 +592,21 @@ __global__ __launch_bounds__(kMKThreads) void ln_tile_kernel(LnTileArgs a) {
   // Row loads first, then the weight prefetch, then the reductions: the norm waits only for the
   // rows, and the weights stream in meanwhile.
   mk_layernorm<true>(a.x, a.gamma, a.beta, nullptr, row0, nrows, a.D, lds,
-                     [&] { mk_prefetch_w<true>(a.w, a.D, n0, lds); });
+                     [&] { mk_prefetch_w<true>(a.w, a.D, n0, 0, a.D / 64, lds); });
   mk_gemm_tile<MODE, true>(nullptr, a.w, a.D, row0, nrows, n0, a.ep, lds);
 }
 
 template <int HD, bool CAUSAL>
 __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
   extern __shared__ __align__(16) half lds[];
-  half* resa = lds;
   half* sk = lds;                     // attention tiles reuse the start of the map
   half* sv = lds + 2 * kBKV * HD;
-  int* sred = (int*)(lds + kLdsHalfs);
+  int* sred = (int*)(lds + kLdsHalfs);                    // 16 ints
+  float2* srow = (float2*)(lds + kLdsHalfs + 32);         // 64 (mean, rstd) pairs
 
   const uint32_t epoch = ld_relaxed(p.ctrl) + 1u;  // this launch's number (workspace starts at 0)
   const AttnArgs aa{p.q, p.k, p.vt, p.mask, p.ctx, p.B, p.S, p.H, p.scale_log2};
+  const int ksw = 64 * p.ksteps;                   // columns of h per FF2 split
 
   for (int t = blockIdx.x; t < p.ntask; t += gridDim.x) {
     trace_stamp(p, t, 1);
@@ -485,7 +629,8 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
     int i0 = t - l * p.per_layer;
     int kind = 0;
     {
-      const int seg[5] = {p.nrb * p.tq, p.B * p.H * p.nqb, p.nrb * p.td, p.nrb * p.tf, p.nrb * p.td};
+      const int seg[5] = {p.nrb * p.tq, p.B * p.H * p.nqb, p.nrb * p.td, p.nrb * p.tf,
+                          p.nrb * p.td * p.ks};
       while (kind < 4 && i0 >= seg[kind]) i0 -= seg[kind++];
     }
     const half* wl = p.w + (size_t)l * p.stride;
@@ -517,16 +662,23 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
       continue;
     }
 
-    // GEMM tasks: i0 = rb * tiles + nt
+    // GEMM tasks: i0 = (rb * tiles + nt) (* ks + split for FF2)
+    int split = 0;
+    if (kind == 4) {
+      split = i0 % p.ks;
+      i0 /= p.ks;
+    }
     const int tiles = (kind == 0) ? p.tq : (kind == 3) ? p.tf : p.td;
     const int rb = i0 / tiles, nt = i0 - rb * tiles;
     const int b = rb / p.nsb, sb = rb - b * p.nsb;
     const int row0 = b * p.S + sb * kMB, nrows = min(kMB, p.S - sb * kMB);
     const int n0 = nt * kNB;
+    const int nkd = p.D / 64;
     EpiArgs ep{};
-    if (kind == 0) {  // QKV
-      const half* W = wl + p.off[2];
-      mk_prefetch_w<true>(W, p.D, n0, lds);
+    if (kind == 0) {  // QKV: LayerNorm 1 folded into W'
+      const half* W = wl + p.off[12];
+      mk_prefetch_w<false>(W, p.D, n0, 0, nkd, lds);
+      const FoldCols f = mk_load_fold((const float*)(wl + p.off[13]), (const float*)(wl + p.off[14]), n0);
       if (l > 0) {
         mk_wait(p, counter(p, l - 1, cFF2, rb), epoch * (uint32_t)p.td);
         // write-after-read on Q/K/V^T: attention of layer l-1 reading rows rb is done
@@ -534,56 +686,90 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
           mk_wait(p, counter(p, l - 1, cATT, b * p.nsb + j), epoch * (uint32_t)p.H);
       }
       trace_stamp(p, t, 2);
-      mk_layernorm<true>(l == 0 ? p.x : p.xa, wl + p.off[0], wl + p.off[1], nullptr, row0, nrows,
-                         p.D, resa);
-      ep.bias = wl + p.off[3];
+      const floatx16 acc = mk_tile_core<false, true>(l == 0 ? p.x : p.xa, p.D, W, p.D, n0, 0, nkd,
+                                                     row0, nrows, lds, srow);
       ep.y = p.q;
       ep.ldy = 3 * p.D;
-      ep.mode = TT_EPI_QKV;
       ep.batch = p.B;
       ep.seq = p.S;
       ep.heads = p.H;
       ep.head_dim = HD;
       ep.d_model = p.D;
-      mk_gemm_tile<TT_EPI_QKV, true>(nullptr, W, p.D, row0, nrows, n0, ep, lds);
+      mk_epilogue_fold<TT_EPI_QKV>(acc, f, srow, ep, row0, nrows, n0);
       mk_signal(counter(p, l, cQKV, rb));
     } else if (kind == 2) {  // OUT
       const half* W = wl + p.off[4];
-      mk_prefetch_w<false>(W, p.D, n0, lds);
+      mk_prefetch_w<false>(W, p.D, n0, 0, nkd, lds);
+      TileCols c;
+      mk_load_bias(c, wl + p.off[5], n0);
       mk_wait(p, counter(p, l, cATT, rb), epoch * (uint32_t)p.H);
       trace_stamp(p, t, 2);
-      ep.bias = wl + p.off[5];
       ep.resid = (l == 0) ? p.x : p.xa;
       ep.valid = p.mask;
       ep.y = p.xa;
       ep.ldy = p.D;
-      ep.mode = TT_EPI_RESID_MASKED;
-      mk_gemm_tile<TT_EPI_RESID_MASKED, false>(p.ctx, W, p.D, row0, nrows, n0, ep, lds);
+      mk_load_resid(c, ep, row0, nrows, n0);
+      const floatx16 acc =
+          mk_tile_core<false, false>(p.ctx, p.D, W, p.D, n0, 0, nkd, row0, nrows, lds, nullptr);
+      mk_epilogue<TT_EPI_RESID_MASKED>(acc, c, ep, row0, nrows, n0);
       mk_signal(counter(p, l, cOUT, rb));
-    } else if (kind == 3) {  // FF1
-      const half* W = wl + p.off[8];
-      mk_prefetch_w<true>(W, p.D, n0, lds);
+    } else if (kind == 3) {  // FF1: LayerNorm 2 folded into W'
+      const half* W = wl + p.off[15];
+      mk_prefetch_w<false>(W, p.D, n0, 0, nkd, lds);
+      const FoldCols f = mk_load_fold((const float*)(wl + p.off[16]), (const float*)(wl + p.off[17]), n0);
       mk_wait(p, counter(p, l, cOUT, rb), epoch * (uint32_t)p.td);
       trace_stamp(p, t, 2);
-      mk_layernorm<true>(p.xa, wl + p.off[6], wl + p.off[7], nullptr, row0, nrows, p.D, resa);
-      ep.bias = wl + p.off[9];
+      const floatx16 acc =
+          mk_tile_core<false, true>(p.xa, p.D, W, p.D, n0, 0, nkd, row0, nrows, lds, srow);
       ep.y = p.hbuf;
       ep.ldy = p.F;
-      ep.mode = TT_EPI_BIAS_GELU;
-      mk_gemm_tile<TT_EPI_BIAS_GELU, true>(nullptr, W, p.D, row0, nrows, n0, ep, lds);
-      mk_signal(counter(p, l, cFF1, rb));
-    } else {  // FF2
+      mk_epilogue_fold<TT_EPI_BIAS_GELU>(acc, f, srow, ep, row0, nrows, n0);
+      mk_signal(counter(p, l, cFF1, rb, nt / p.ksteps));
+    } else {  // FF2 split `split`: columns [split ksw, (split + 1) ksw) of h and W2
       const half* W = wl + p.off[10];
-      mk_prefetch_w<false>(W, p.F, n0, lds);
-      mk_wait(p, counter(p, l, cFF1, rb), epoch * (uint32_t)p.tf);
+      const int k0 = split * ksw;
+      const bool reducer = split == p.ks - 1;
+      mk_prefetch_w<false>(W, p.F, n0, k0, p.ksteps, lds);
+      TileCols c;
+      if (reducer) mk_load_bias(c, wl + p.off[11], n0);
+      mk_wait(p, counter(p, l, cFF1, rb, split), epoch * (uint32_t)p.ksteps);
       trace_stamp(p, t, 2);
-      ep.bias = wl + p.off[11];
       ep.resid = p.xa;
       ep.valid = p.mask;
       ep.y = p.xa;
       ep.ldy = p.D;
-      ep.mode = TT_EPI_MASKED_RESID;
-      mk_gemm_tile<TT_EPI_MASKED_RESID, false>(p.hbuf, W, p.F, row0, nrows, n0, ep, lds);
+      if (reducer) mk_load_resid(c, ep, row0, nrows, n0);
+      floatx16 acc =
+          mk_tile_core<false, false>(p.hbuf, p.F, W, p.F, n0, k0, p.ksteps, row0, nrows, lds, nullptr);
+      // Split-K: splits 0 .. ks-2 store fp32 partial tiles (per lane, in accumulator order) and
+      // count their arrival; the last split (numbered after them, so it may wait for them) adds
+      // the partials and its own accumulator in split order and runs the epilogue.
+      float* part = p.part + (size_t)(rb * p.td + nt) * p.ks * (kMKThreads * 16);
+      if (!reducer) {
+        floatx4* mine = (floatx4*)(part + (size_t)split * (kMKThreads * 16)) + 4 * threadIdx.x;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          mine[g] = floatx4{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
+        mk_signal(counter(p, l, cFF2T, rb, nt));
+        trace_stamp(p, t, 3);
+        continue;
+      }
+      if (p.ks > 1) {
+        mk_wait(p, counter(p, l, cFF2T, rb, nt), epoch * (uint32_t)(p.ks - 1));
+        floatx4 sum[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) sum[g] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < p.ks - 1; ++j) {
+          const floatx4* src = (const floatx4*)(part + (size_t)j * (kMKThreads * 16)) + 4 * threadIdx.x;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) sum[g] += src[g];
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[4 * g + e] = sum[g][e] + acc[4 * g + e];
+      }
+      mk_epilogue<TT_EPI_MASKED_RESID>(acc, c, ep, row0, nrows, n0);
       mk_signal(counter(p, l, cFF2, rb));
     }
     trace_stamp(p, t, 3);
@@ -625,8 +811,18 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
 // ---- host side ----
 
 struct MegaLayout {
-  size_t xa, ctx, qkv, hbuf, cnt, ctrl, bytes;
+  size_t xa, ctx, qkv, hbuf, part, cnt, ctrl, bytes;
 };
+
+// FF2 splits of K = F: the most (up to kSub) that divide F / 64 into at least kMinSplitSteps
+// K steps each.
+static int ff2_splits(int64_t F) {
+  const int64_t nk = F / 64;
+  int best = 1;
+  for (int s = 2; s <= kSub; ++s)
+    if (nk % s == 0 && nk / s >= kMinSplitSteps) best = s;
+  return best;
+}
 
 static size_t al256(size_t v) { return (v + 255) / 256 * 256; }
 
@@ -643,7 +839,9 @@ static MegaLayout mega_layout(int64_t B, int64_t S, int64_t D, int64_t F, int64_
   m.ctx = take(T * D * 2);
   m.qkv = take((2 * T * D + B * D * Sp) * 2);
   m.hbuf = take(T * F * 2);
-  m.cnt = take((size_t)L * kNumCounters * nrb * 4);
+  const int ks = ff2_splits(F);
+  m.part = take(ks > 1 ? (size_t)nrb * (D / kNB) * ks * kMKThreads * 16 * 4 : 0);
+  m.cnt = take((size_t)L * kNumCounters * nrb * kSub * 4);
   m.ctrl = take(64);
   m.bytes = o;
   return m;
@@ -656,7 +854,7 @@ size_t megakernel_workspace_bytes(int B, int S, int D, int F, int L) {
 int megakernel_supported(int B, int S, int D, int H, int F, int L) {
   TT_REQUIRE(D / H == 32 || D / H == 64, "megakernel: head_dim %d not in {32, 64}", D / H);
   TT_REQUIRE(D % 64 == 0 && F % 64 == 0, "megakernel: d_model and ffn_dim must be multiples of 64");
-  TT_REQUIRE(D <= kMaxD, "megakernel: d_model %d > %d (the LayerNorm'd operand lives in LDS)", D,
+  TT_REQUIRE(D <= kMaxD, "megakernel: d_model %d > %d (one dependency counter per 64 columns)", D,
              kMaxD);
   TT_REQUIRE((int64_t)B * S <= (1 << 20), "megakernel: too many tokens for the persistent plan");
   (void)L;
@@ -665,7 +863,7 @@ int megakernel_supported(int B, int S, int D, int H, int F, int L) {
 
 template <int HD, bool CAUSAL>
 static int launch_mega(MegaParams& p, hipStream_t stream) {
-  const size_t lds = kLdsHalfs * sizeof(half) + 64;
+  const size_t lds = kLdsHalfs * sizeof(half) + 64 + 64 * sizeof(float2);
   static_assert(2 * kBKV * HD * 2 <= kLdsHalfs, "attention tiles must fit the LDS map");
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
@@ -681,10 +879,10 @@ static int launch_mega(MegaParams& p, hipStream_t stream) {
   int dev = 0, cus = 0;
   TT_HIP(hipGetDevice(&dev));
   TT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-  // As many workgroups as the widest stage has tasks, at most one per CU (all resident).
-  const int widest = std::max({p.nrb * p.tq, p.B * p.H * p.nqb, p.nrb * p.tf, p.nrb * p.td});
+  // One workgroup per task up to one per CU (all resident): with few tasks every workgroup
+  // prefetches its weights at once, with many each runs a task of every stage in turn.
   if (per_cu < 1) return fail(TT_ERR_HIP, "megakernel: a workgroup does not fit a CU");
-  const int grid = std::max(1, std::min(widest, cus));
+  const int grid = std::max(1, std::min(p.ntask, cus));
   hipLaunchKernelGGL((megakernel<HD, CAUSAL>), dim3(grid), dim3(kMKThreads), lds, stream, p);
   return launch_status("megakernel");
 }
@@ -725,7 +923,7 @@ int launch_ln_tile(const half* x, const half* gamma, const half* beta, const hal
 int megakernel_tasks(int B, int S, int D, int H, int F, int L) {
   const int nsb = (S + kMB - 1) / kMB, nrb = B * nsb, nqb = (S + kQB - 1) / kQB;
   const int per_layer = nrb * (3 * D / kNB) + B * H * nqb + nrb * (D / kNB) + nrb * (F / kNB) +
-                        nrb * (D / kNB);
+                        nrb * (D / kNB) * ff2_splits(F);
   return L * per_layer + nrb;
 }
 
@@ -739,7 +937,8 @@ void megakernel_set_spin_limit(int64_t limit) {
   g_spin_limit = limit < 0 ? kSpinLimit : (uint32_t)std::min<int64_t>(limit, 0xFFFFFFFFll);
 }
 
-int launch_megakernel(const half* weights, const int64_t off[12], int64_t stride, int64_t final_off,
+int launch_megakernel(const half* weights, const int64_t off[TT_LAYER_SEGMENTS], int64_t stride,
+                      int64_t final_off,
                       const half* x, const uint8_t* mask, half* y, char* workspace,
                       int64_t workspace_bytes, int B, int S, int D, int H, int F, int L, int causal,
                       uint64_t* trace, hipStream_t stream) {
@@ -762,6 +961,7 @@ int launch_megakernel(const half* weights, const int64_t off[12], int64_t stride
   p.k = p.q + (size_t)B * S * D;
   p.vt = p.q + 2 * (size_t)B * S * D;
   p.hbuf = (half*)(workspace + m.hbuf);
+  p.part = (float*)(workspace + m.part);
   p.cnt = (uint32_t*)(workspace + m.cnt);
   p.ctrl = (uint32_t*)(workspace + m.ctrl);
   p.trace = trace;
@@ -779,7 +979,9 @@ int launch_megakernel(const half* weights, const int64_t off[12], int64_t stride
   p.tq = 3 * D / kNB;
   p.td = D / kNB;
   p.tf = F / kNB;
-  p.per_layer = p.nrb * p.tq + B * H * p.nqb + p.nrb * p.td + p.nrb * p.tf + p.nrb * p.td;
+  p.ks = ff2_splits(F);
+  p.ksteps = F / 64 / p.ks;
+  p.per_layer = p.nrb * p.tq + B * H * p.nqb + p.nrb * p.td + p.nrb * p.tf + p.nrb * p.td * p.ks;
   p.ntask = L * p.per_layer + p.nrb;
   p.scale_log2 = (1.0f / sqrtf((float)(D / H))) * 1.4426950408889634f;
   const int hd = D / H;
