@@ -699,16 +699,17 @@ static int run_small(int mode, const half* x, const half* w, int m, int n, int k
 
 // Narrow-tile GEMM for grids that would leave most CUs idle (few tokens): 32 x 32 output tiles, so
 // four times as many blocks as 64 x 64 tiles pull operands (each CU's streaming rate is set by the
-// bytes it keeps in flight), with the K range split over the block's four waves.  Each wave loads
+// bytes it keeps in flight), with the K range split over the block's NW waves.  Each wave loads
 // its W and X fragments straight into registers (lane l: row l % 32, 8 K values at 8 (l / 32)),
-// NPF K steps ahead, and accumulates one 32 x 32 MFMA tile; the four partial tiles are summed in
-// LDS in wave order (deterministic) and the epilogue runs 4 outputs per thread.
+// NPF K steps ahead, and accumulates one 32 x 32 MFMA tile; the NW partial tiles are summed in
+// LDS in wave order (deterministic) and the epilogue runs 4 outputs per thread on the first 256
+// threads.  Long K (few blocks, each streaming many bytes) uses 8 waves with 8 steps per buffer,
+// so a block keeps 128 KiB of operands in flight.
 constexpr int kNarrow = 32;
-template <int MODE>
-__global__ __launch_bounds__(256) void gemm_narrow_kernel(const half* __restrict__ X,
-                                                          const half* __restrict__ W, int M, int N,
-                                                          int K, EpiArgs ep) {
-  constexpr int NPF = 4;  // K steps of 16 per register buffer
+template <int MODE, int NW, int NPF>
+__global__ __launch_bounds__(64 * NW) void gemm_narrow_kernel(const half* __restrict__ X,
+                                                              const half* __restrict__ W, int M,
+                                                              int N, int K, EpiArgs ep) {
   const int tiles_n = N / kNarrow;
   const int tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
   const int m0 = tm * kNarrow, n0 = tn * kNarrow;
@@ -716,10 +717,11 @@ __global__ __launch_bounds__(256) void gemm_narrow_kernel(const half* __restrict
   const int r = lane & 31, kh = 8 * (lane >> 5);
   const half* xr = X + (size_t)min(m0 + r, M - 1) * K + kh;
   const half* wr = W + (size_t)(n0 + r) * K + kh;
-  const int steps = K / 16 / 4;          // K steps of this wave (K % 64 == 0)
+  const int steps = K / 16 / NW;         // K steps of this wave (K % (16 NW) == 0)
   const int kbeg = wave * steps * 16;
   // epilogue mapping (below): thread -> row ml, 4 columns nl; 8 aligned threads per row
-  const int ml = threadIdx.x >> 3, nl = 4 * (threadIdx.x & 7);
+  const int et = threadIdx.x & 255;
+  const int ml = et >> 3, nl = 4 * (et & 7);
   const LnPre pre = ln_pre4<MODE, 8>(ep, min(m0 + ml, M - 1), n0 + nl, K);
   floatx16 acc;
 #pragma unroll
@@ -748,41 +750,47 @@ __global__ __launch_bounds__(256) void gemm_narrow_kernel(const half* __restrict
     mma(1, s0 + NPF);
   }
   // acc[4g + e] = C[m0 + r][n0 + 8g + 4 (lane / 32) + e]
-  __shared__ __align__(16) float part[4][kNarrow][kNarrow];
+  __shared__ __align__(16) float part[NW][kNarrow][kNarrow];
 #pragma unroll
   for (int g = 0; g < 4; ++g)
     *(floatx4*)&part[wave][r][8 * g + 4 * (lane >> 5)] =
         floatx4{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
   __syncthreads();
-  if (m0 + ml >= M) return;
+  if (threadIdx.x >= 256 || m0 + ml >= M) return;
   float sum[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e)
-    sum[e] = ((part[0][ml][nl + e] + part[1][ml][nl + e]) + part[2][ml][nl + e]) + part[3][ml][nl + e];
+  for (int e = 0; e < 4; ++e) {
+    float v = part[0][ml][nl + e];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += part[w][ml][nl + e];
+    sum[e] = v;
+  }
   epilogue4<MODE, 8>(ep, m0 + ml, n0 + nl, sum, pre);
+}
+
+// Long K: 8 waves (K % 128 == 0 and more than two 4-step buffers per wave at 4 waves).
+static bool narrow_long_k(int k) { return k % 128 == 0 && k / 64 > 8; }
+
+template <int MODE>
+static void launch_narrow_mode(dim3 grid, const half* x, const half* w, int m, int n, int k,
+                               const EpiArgs& ep, hipStream_t stream) {
+  if (narrow_long_k(k))
+    hipLaunchKernelGGL((gemm_narrow_kernel<MODE, 8, 8>), grid, dim3(512), 0, stream, x, w, m, n, k, ep);
+  else
+    hipLaunchKernelGGL((gemm_narrow_kernel<MODE, 4, 4>), grid, dim3(256), 0, stream, x, w, m, n, k, ep);
 }
 
 static int run_narrow(int mode, const half* x, const half* w, int m, int n, int k,
                       const EpiArgs& ep, hipStream_t stream) {
   const long blocks = (long)((m + kNarrow - 1) / kNarrow) * (n / kNarrow);
   TT_REQUIRE(blocks < (1L << 31), "linear: grid too large");
-  const dim3 grid((unsigned)blocks), block(256);
+  const dim3 grid((unsigned)blocks);
   switch (mode) {
-    case TT_EPI_BIAS:
-      hipLaunchKernelGGL(gemm_narrow_kernel<TT_EPI_BIAS>, grid, block, 0, stream, x, w, m, n, k, ep);
-      break;
-    case TT_EPI_BIAS_GELU:
-      hipLaunchKernelGGL(gemm_narrow_kernel<TT_EPI_BIAS_GELU>, grid, block, 0, stream, x, w, m, n, k, ep);
-      break;
-    case TT_EPI_RESID_MASKED:
-      hipLaunchKernelGGL(gemm_narrow_kernel<TT_EPI_RESID_MASKED>, grid, block, 0, stream, x, w, m, n, k, ep);
-      break;
-    case TT_EPI_MASKED_RESID:
-      hipLaunchKernelGGL(gemm_narrow_kernel<TT_EPI_MASKED_RESID>, grid, block, 0, stream, x, w, m, n, k, ep);
-      break;
-    default:
-      hipLaunchKernelGGL(gemm_narrow_kernel<TT_EPI_QKV>, grid, block, 0, stream, x, w, m, n, k, ep);
-      break;
+    case TT_EPI_BIAS: launch_narrow_mode<TT_EPI_BIAS>(grid, x, w, m, n, k, ep, stream); break;
+    case TT_EPI_BIAS_GELU: launch_narrow_mode<TT_EPI_BIAS_GELU>(grid, x, w, m, n, k, ep, stream); break;
+    case TT_EPI_RESID_MASKED: launch_narrow_mode<TT_EPI_RESID_MASKED>(grid, x, w, m, n, k, ep, stream); break;
+    case TT_EPI_MASKED_RESID: launch_narrow_mode<TT_EPI_MASKED_RESID>(grid, x, w, m, n, k, ep, stream); break;
+    default: launch_narrow_mode<TT_EPI_QKV>(grid, x, w, m, n, k, ep, stream); break;
   }
   return launch_status("gemm_narrow_kernel");
 }

@@ -115,6 +115,23 @@ __device__ __forceinline__ uint32_t* counter(const MegaParams& p, int layer, int
   return p.cnt + (((size_t)layer * kNumCounters + kind) * p.nrb + rb) * kSub + sub;
 }
 
+// Agent-scope release / acquire for one thread, with the cache maintenance made synchronous.
+// The fence emits the L2 write-back (release) or the L1 / L2 invalidate (acquire); both are
+// vector-memory operations that complete asynchronously, and the compiler does not always keep
+// a wait for them (the write-back was seen issued right before the counter's atomic add with
+// nothing in between, and consumers then read stale rows).  Waiting for vmcnt(0) after the fence
+// makes the write-back complete before the counter update that follows, and the invalidate
+// complete before the workgroup barrier after which the other waves load.
+__device__ __forceinline__ void release_agent() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+__device__ __forceinline__ void acquire_agent() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 // Block-wide: wait until *c has reached `target` (mod 2^32), bounded.  Thread 0 polls and then
 // performs the agent-scope acquire (it invalidates this CU's L1 and the XCD's L2 copies of other
 // XCDs' data for the whole workgroup); the barrier orders every other wave's later loads after
@@ -130,7 +147,7 @@ __device__ void mk_wait(const MegaParams& p, const uint32_t* c, uint32_t target)
       }
       __builtin_amdgcn_s_sleep(1);
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    acquire_agent();
   }
   __syncthreads();
 }
@@ -142,7 +159,7 @@ __device__ void mk_signal(uint32_t* c) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    release_agent();
     __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -653,7 +670,7 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       if (threadIdx.x == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        release_agent();
         for (int j = 2 * qb; j < min(2 * qb + 2, p.nsb); ++j)
           __hip_atomic_fetch_add(counter(p, l, cATT, b * p.nsb + j), 1u, __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
@@ -779,16 +796,20 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
   // finish count (every workgroup read the epoch before it arrives here; the next launch is
   // stream-ordered after this one).  If a dependency wait of this or an earlier launch gave up
   // (error word set), the results are invalid: that workgroup then overwrites all of y with NaN
-  // (fp16 0x7E00) -- the arrivals are acq_rel, so every other workgroup's writes of y precede it
-  // -- and the host sees the error word on its next health check.
+  // (fp16 0x7E00) -- every arrival is preceded by a release and the last one acquires, so every
+  // other workgroup's writes of y precede it -- and the host sees the error word on its next
+  // health check.
   __shared__ uint32_t last;
   __syncthreads();
   if (threadIdx.x == 0) {
     last = 0;
-    const uint32_t old = __hip_atomic_fetch_add(p.ctrl + 1, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    release_agent();
+    const uint32_t old = __hip_atomic_fetch_add(p.ctrl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old + 1u == gridDim.x) {
+      acquire_agent();
       __hip_atomic_store(p.ctrl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(p.ctrl, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      release_agent();
+      __hip_atomic_store(p.ctrl, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const uint32_t err = ld_relaxed(p.ctrl + 2);
       last = err != 0 ? 1u : 0u;
       // mirror the error flag into the caller's pinned host word, if one is attached
