@@ -21,12 +21,15 @@
 // Residency comes from the launch size: G <= the number of CUs and a workgroup's 144 KiB of LDS
 // fits one per CU, so on a device not shared with other kernels every workgroup is dispatched at
 // once.  (A cooperative launch would guarantee it formally but costs ~17 us more per launch on
-// MI355X -- measured -- which is more than the forward of the small shapes this plan is for.)  Dependencies are per (layer, kind, row block) counters in the workspace that
-// only ever grow; a launch waits for `epoch * count`, where the epoch (launch number) is kept in
-// the workspace and advanced by the last workgroup to finish, so no counter is ever reset (the
+// MI355X -- measured -- which is more than the forward of the small shapes this plan is for.)
+// Dependencies are per (layer, kind, row block, sub-index) counters in the workspace that only
+// ever grow; a launch waits for `epoch * count`, where the epoch (launch number) is kept in the
+// workspace and advanced by the last workgroup to finish, so no counter is ever reset (the
 // workspace must be zero-filled once, before its first use).  Hand-offs are agent-scope
-// release/acquire (the XCDs have separate L2s).  Every spin-wait is bounded: on expiry the kernel
-// records an error in the workspace and all later waits fall through, so every wave exits.
+// release/acquire (the XCDs have separate L2s) whose L2 write-back / invalidate is waited for
+// before the counter changes / before the data is read.  Every spin-wait is bounded: on expiry
+// the kernel records an error in the workspace and all later waits fall through, so every wave
+// exits.
 //
 // Write-after-read: Q/K/V^T are single buffers, so QKV(l, rb) also waits for every attention
 // task of layer l-1 whose keys include rb.  Every other buffer's next writer already depends
@@ -35,8 +38,8 @@
 // The tasks are latency-bound (a 64 x 64 tile has 4 MFMAs per wave per K step), so the GEMM
 // tiles keep up to 8 K steps of copies in flight (global -> LDS, waited per step with vmcnt),
 // weights are prefetched before a task waits for its inputs, each task issues all of its memory
-// traffic as early as its dependencies allow, and LayerNorm row sums use DPP / lane-swap
-// reductions (no LDS round trips).
+// traffic as early as its dependencies allow, and row statistics use DPP quad reductions (no LDS
+// round trips).
 #include "attention_block.hpp"
 #include "kernels.hpp"
 
@@ -51,7 +54,7 @@ namespace {
 constexpr int kMB = 64;            // rows per row block
 constexpr int kQB = 128;           // queries per attention block (= attention_block's tile)
 constexpr int kNB = 64;            // columns per GEMM tile
-constexpr int kMaxD = 512;         // LN'd A operand resident in LDS: 64 x D halfs
+constexpr int kMaxD = 512;         // fused-LN tiles: LN'd A operand resident in LDS, 64 x D halfs
 constexpr int kMKThreads = 256;
 constexpr uint32_t kSpinLimit = 1u << 22;  // polls (each followed by s_sleep 1) per wait
 
@@ -306,8 +309,8 @@ __device__ __forceinline__ void mk_prefetch_w(const half* W, int ld, int n0, int
 }
 
 // Accumulator of the 64 x 64 tile: sum over K steps s < nk of A[row0 + m][k0 + 64 s ..] .
-// W[n0 + n][k0 + 64 s ..] (row strides lda, ldw).  A comes from `A` (streamed, RESA == false) or from the resident
-// LayerNorm'd area (RESA == true).  The W copies of the first NS - 1 steps must have been issued
+// W[n0 + n][k0 + 64 s ..] (row strides lda, ldw).  A comes from `A` (streamed, RESA == false)
+// or from the resident LayerNorm'd area (RESA == true, the fused-LN plan's tiles).  The W copies of the first NS - 1 steps must have been issued
 // by mk_prefetch_w<RESA> with the same arguments; loads the caller issues between the two are
 // complete when the first step is.  Four waves in 2 x 2, each a 32 x 32 MFMA block (W as the
 // MFMA's A operand, so the accumulator is C^T): acc[4 g + e] = C[32 wm + lane % 32]
