@@ -82,8 +82,11 @@ def test_workspace_bytes_monotone_and_validated():
 
 def test_plan_resolution():
     # measured on MI355X: LN fused into the QKV / ffn_in tiles wins only for d_model <= 128 with
-    # few tokens; C1 / C2 run layer-wise (narrow GEMM tiles); the megakernel is only explicit
-    assert _lib.resolve_plan(1, 64, 256, 8, 1024, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE      # C2
+    # few tokens; C2 (64 tokens) runs the persistent megakernel, C1 layer-wise (narrow GEMM tiles)
+    assert _lib.resolve_plan(1, 64, 256, 8, 1024, _lib.PLAN_AUTO) == _lib.PLAN_MEGAKERNEL     # C2
+    assert _lib.resolve_plan(2, 32, 256, 4, 1024, _lib.PLAN_AUTO) == _lib.PLAN_MEGAKERNEL
+    assert _lib.resolve_plan(1, 65, 256, 8, 1024, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE
+    assert _lib.resolve_plan(1, 64, 256, 16, 1024, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE    # hd 16
     assert _lib.resolve_plan(4, 128, 256, 4, 1024, _lib.PLAN_AUTO) == _lib.PLAN_LAYERWISE     # C1
     assert _lib.resolve_plan(1, 128, 128, 4, 128, _lib.PLAN_AUTO) == _lib.PLAN_FUSED_LN       # case 2
     assert _lib.resolve_plan(1, 64, 256, 8, 1024, _lib.PLAN_MEGAKERNEL) == _lib.PLAN_MEGAKERNEL

@@ -78,8 +78,10 @@ struct AttnArgs {
 
 // One (sequence b, head h, 128-query tile qt) attention block on 256 threads.  kv_end is
 // 1 + the index of the last valid key of sequence b (S without a mask) and `prefix` says whether
-// the valid keys form a prefix; sk_base / sv_base are 2 * 64 * HD halfs of LDS each.
-template <int HD, bool CAUSAL>
+// the valid keys form a prefix; sk_base / sv_base are 2 * 64 * HD halfs of LDS each.  POLICY is
+// the cache policy of the Q, K and V^T loads (kLoadDevice when other workgroups of the same
+// launch wrote them).
+template <int HD, bool CAUSAL, int POLICY = kLoadDefault>
 __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int qt, int kv_end,
                                                 bool prefix, half* sk_base, half* sv_base) {
   static_assert(HD == 32 || HD == 64 || HD == 128 || HD == 256, "MFMA attention head_dim");
@@ -140,11 +142,11 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
 #pragma unroll
     for (int c = 0; c < KCOPIES; ++c) {
       const int key = min(t0 + krow[c], S - 1);  // rows past S load valid memory, never used
-      lds_copy16(Kbh + (size_t)key * HD + koff[c], &sk[st][(wave * KCOPIES + c) * 512]);
+      lds_copy16<POLICY>(Kbh + (size_t)key * HD + koff[c], &sk[st][(wave * KCOPIES + c) * 512]);
     }
 #pragma unroll
     for (int c = 0; c < VCOPIES; ++c)
-      lds_copy16(Vbh + voff[c] + t0, &sv[st][(wave * VCOPIES + c) * 512]);
+      lds_copy16<POLICY>(Vbh + voff[c] + t0, &sv[st][(wave * VCOPIES + c) * 512]);
   };
   // V^T columns of keys >= S (padding of the last, partial tile) are cleared in LDS so that
   // 0-probability keys contribute 0 * 0, whatever the padding memory holds.
@@ -159,10 +161,17 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
   half8 qf[KSTEPS];
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) {
-    if (q < S) qf[kk] = *(const half8*)(Qbh + (size_t)q * HD + 16 * kk + 8 * hf);
-    else
+    if (q < S) {
+      if constexpr (POLICY == kLoadDefault) {
+        qf[kk] = *(const half8*)(Qbh + (size_t)q * HD + 16 * kk + 8 * hf);
+      } else {  // one (b, h) plane of Q is S * HD halfs, far below 4 GiB
+        const __amdgpu_buffer_rsrc_t qr = buffer_rsrc(Qbh, (uint32_t)S * HD * 2);
+        qf[kk] = __builtin_bit_cast(half8, load16<POLICY>(qr, (uint32_t)(q * HD + 16 * kk + 8 * hf) * 2));
+      }
+    } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) qf[kk][e] = (half)0.f;
+    }
   }
 
   floatx16 o[DB];

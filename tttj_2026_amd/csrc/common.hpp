@@ -81,11 +81,32 @@ __device__ __forceinline__ void lds_barrier() {
   raw_barrier();
 }
 
+// Cache policy of a load (the instruction's cache-control bits): kLoadDefault may hit in the CU's
+// L1; kLoadDevice (sc1, device scope) misses the L1 and is served by the L2 of the XCD the CU
+// belongs to.  Data written earlier in the same launch by a workgroup on another CU of the same
+// XCD is in that shared L2 once the writer's stores have completed, while the reader's L1 may
+// still hold older copies of those lines, so such data is read with kLoadDevice.
+constexpr int kLoadDefault = 0;
+constexpr int kLoadDevice = 16;
+
 // Global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane l writes LDS bytes
 // [16 l, 16 l + 16) after the wave-uniform destination `lds_dst`.
+template <int POLICY = kLoadDefault>
 __device__ __forceinline__ void lds_copy16(const half* src, half* lds_dst) {
   __builtin_amdgcn_global_load_lds((const void*)src,
-                                   (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
+                                   (__attribute__((address_space(3))) void*)lds_dst, 16, 0, POLICY);
+}
+
+// Raw buffer resource over [base, base + bytes): stride 0; 0x00020000 is the data-format word
+// for untyped 32-bit accesses.  `base` must be wave-uniform.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+// 16-byte load at byte offset `off` of the buffer `r` with cache policy POLICY.
+template <int POLICY>
+__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POLICY);
 }
 
 template <int CTRL>

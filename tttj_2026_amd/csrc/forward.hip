@@ -130,11 +130,12 @@ extern "C" int tt_pack_derived(void* weights, int d_model, int ffn_dim, int num_
                              (hipStream_t)stream);
 }
 
-// Token count up to which the automatic plan runs the persistent megakernel.  Measured on MI355X
-// (C1: B4 S128 D256, C2: B1 S64 D256) the megakernel is still slower than the layer-wise plan,
-// whose back-to-back launches pipeline with almost no gap, so the automatic choice is layer-wise
-// everywhere until that changes; the megakernel is selected explicitly with TT_PLAN_MEGAKERNEL.
-static constexpr int64_t kMegaMaxTokens = 0;
+// Token count up to which the automatic plan runs the persistent megakernel (d_model >= 256).
+// Measured on MI355X (same-process medians): C2 (B1 S64 D256 H8 F1024 L4) 88.7 us against 91.8
+// for the layer-wise plan, whose back-to-back launches pipeline with almost no gap; C1 (B4 S128,
+// 512 tokens) 60.5 against 60.0, so from there on the layer-wise plan stays the choice.
+static constexpr int64_t kMegaMaxTokens = 64;
+static constexpr int kMegaMinDModel = 256;
 static constexpr int kMegaMaxDModel = 512;  // the megakernel keeps a LayerNorm'd 64 x D tile in LDS
 // The automatic plan computes LN1 / LN2 inside the QKV / ffn_in 64 x 64 tiles (fewer launches on
 // the latency-bound path) only for narrow models with few tokens: measured on MI355X, d_model 128
@@ -152,7 +153,8 @@ static int resolve_plan(int plan, int B, int S, int D, int H, int F) {
   const int64_t T = (int64_t)B * S;
   const bool tiles64 = D % 64 == 0 && F % 64 == 0 && D <= kMegaMaxDModel;
   const int hd = H > 0 ? D / H : 0;
-  if (T <= kMegaMaxTokens && tiles64 && (hd == 32 || hd == 64)) return TT_PLAN_MEGAKERNEL;
+  if (T <= kMegaMaxTokens && D >= kMegaMinDModel && tiles64 && (hd == 32 || hd == 64))
+    return TT_PLAN_MEGAKERNEL;
   if (tiles64 && D <= kFusedLnMaxDModel && T <= kFusedLnMaxTokens) return TT_PLAN_FUSED_LN;
   return TT_PLAN_LAYERWISE;
 }

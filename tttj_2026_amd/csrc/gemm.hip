@@ -137,12 +137,8 @@ __device__ void fill_padded_tile(const EpiArgs& ep, int M, int m0, int n0) {
 // buffer loads and ds_write_b128, two K stages ahead in two register sets, so a CU keeps three K
 // stages of operands in flight instead of one.  That is what a grid of about one tile per CU
 // streaming a long K needs (its time is the latency of the bytes each CU has in flight); with
-// several tiles per CU the direct global -> LDS copies (PATH = 0) are as fast.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const half* base, int bytes) {
-  // raw buffer: stride 0, num_records = bytes; 0x00020000 is the gfx9 data-format word for
-  // untyped 32-bit accesses
-  return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, bytes, 0x00020000);
-}
+// several tiles per CU the direct global -> LDS copies (PATH = 0) are as fast.  (buffer_rsrc:
+// common.hpp.)
 
 // Blocks of NW waves (4: a 2 x 2 wave grid; 8: 4 x 2, i.e. four waves along M), each wave owning
 // a (BM / (NW / 2)) x (BN / 2) block of C as FM x FN 32x32 MFMA tiles.  Two 4-wave blocks of up to

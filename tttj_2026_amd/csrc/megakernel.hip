@@ -15,21 +15,33 @@
 //   FIN(rb)          y[rb] = mask(final_norm(xa[rb]))
 // No task waits for a LayerNorm: the norms of QKV / FF1 ride on the GEMM's own A stream.  An FF2
 // split waits only for the FF1 tiles of its K range.
-// Tasks are numbered in a topological order and handed out statically (task t to workgroup
-// t mod G).  Every task waits only on tasks numbered before it, and all G workgroups are
-// resident at once, so the smallest unfinished task can always run: the DAG cannot deadlock.
-// Residency comes from the launch size: G <= the number of CUs and a workgroup's 144 KiB of LDS
-// fits one per CU, so on a device not shared with other kernels every workgroup is dispatched at
-// once.  (A cooperative launch would guarantee it formally but costs ~17 us more per launch on
-// MI355X -- measured -- which is more than the forward of the small shapes this plan is for.)
+// XCD-local hand-off.  The eight XCDs of an MI355X have separate L2 caches; a workgroup's stores
+// reach its own XCD's L2 (the vector L1 writes through), while making them visible to another
+// XCD takes an L2 write-back and an invalidate, which cost several microseconds per hand-off when
+// many workgroups do them at once (measured).  So sequence b belongs to XCD b mod nx and every
+// task of the sequence runs on that XCD's workgroups: data only moves through the shared L2.  A
+// producer waits for its stores (s_waitcnt vmcnt(0)) and bumps a dependency counter; a consumer
+// polls the counter and reads produced data with device-scope loads (sc1), which skip its own
+// L1 (it may hold stale copies of those lines) and are served by the L2.  A workgroup reads the
+// XCD it runs on from the hardware register XCC_ID and draws a rank on it from that XCD's ticket
+// counter (the grid is nx W workgroups, which dispatch deals round-robin over the XCDs, so every
+// XCD gets W of them); the workgroups of an XCD take turns over the tasks of its sequences in list
+// order (task v of the XCD's list to rank v mod W).  Without a known XCD count the same tasks run
+// over all workgroups with agent-scope release / acquire hand-offs (L2 write-back before the
+// counter changes, invalidate before the data is read).
+// Tasks are listed in a topological order and every task waits only on tasks listed before it;
+// all workgroups are resident at once, so the earliest unfinished task can always run: the DAG
+// cannot deadlock.  Residency comes from the launch size: at most one workgroup per CU, whose
+// 144 KiB of LDS fits one per CU, so on a device not shared with other kernels every workgroup
+// is dispatched at once.  (A cooperative launch would guarantee it formally but costs ~17 us more
+// per launch on MI355X -- measured -- which is more than the forward of the small shapes this
+// plan is for.)
 // Dependencies are per (layer, kind, row block, sub-index) counters in the workspace that only
 // ever grow; a launch waits for `epoch * count`, where the epoch (launch number) is kept in the
 // workspace and advanced by the last workgroup to finish, so no counter is ever reset (the
-// workspace must be zero-filled once, before its first use).  Hand-offs are agent-scope
-// release/acquire (the XCDs have separate L2s) whose L2 write-back / invalidate is waited for
-// before the counter changes / before the data is read.  Every spin-wait is bounded: on expiry
-// the kernel records an error in the workspace and all later waits fall through, so every wave
-// exits.
+// workspace must be zero-filled once, before its first use).  Every spin-wait is bounded: on
+// expiry the kernel records an error in the workspace and all later waits fall through, so every
+// wave exits.
 //
 // Write-after-read: Q/K/V^T are single buffers, so QKV(l, rb) also waits for every attention
 // task of layer l-1 whose keys include rb.  Every other buffer's next writer already depends
@@ -76,7 +88,7 @@ static_assert(kResA + kRingW * kStepW <= kLdsHalfs && kRingAW * kStepAW <= kLdsH
 enum Counter : int { cQKV = 0, cATT, cOUT, cFF1, cFF2, cFF2T, kNumCounters };
 constexpr int kSub = 8;            // >= FF2 splits and >= d_model / 64 (d_model <= kMaxD)
 static_assert(kSub * kNB >= kMaxD, "one FF2T sub-counter per output tile of a row block");
-constexpr int kMinSplitSteps = 4;  // K steps (of 64) per FF2 split at least
+constexpr int kMinSplitSteps = 8;  // K steps (of 64) per FF2 split at least
 
 struct MegaParams {
   const half* w;
@@ -89,15 +101,23 @@ struct MegaParams {
   float* part;      // FF2 split partials: [nrb][td][ks][256 lanes x 16] fp32
   uint32_t* cnt;    // [L][kNumCounters][nrb][kSub]
   uint32_t* ctrl;   // [0] epoch, [1] finished workgroups, [2] error flag, [4..5] host mirror
-                    // address of the error flag (0: none), set by megakernel_attach_status
+                    // address of the error flag (0: none), set by megakernel_attach_status,
+                    // [8 + x] ticket counter of XCD x (XCD-local plan)
   uint64_t* trace;  // optional: 4 words per task (task | wg << 32, start, ready, end) or nullptr
   uint32_t spin_limit;  // polls per dependency wait before it gives up (kSpinLimit by default)
   int B, S, D, H, F, L, causal;
   int nsb, nqb, nrb, tq, td, tf;  // row / query blocks per sequence, row blocks, N tiles
   int ks, ksteps;                 // FF2 splits of K = ffn_dim, K steps (of 64) per split
   int per_layer, ntask;
+  int nx;                         // XCDs (XCD-local plan; <= 8, one ticket word each)
   float scale_log2;
 };
+
+// The launch parameters are read in place from the kernel-argument segment through a pointer in
+// the constant address space (scalar loads).  The persistent loop re-derives that pointer per task
+// (an opaque copy), so a task reloads the fields it uses instead of the compiler keeping every
+// field of every task kind live in registers across the loop.
+typedef const __attribute__((address_space(4))) MegaParams MPc;
 
 __device__ __forceinline__ uint32_t ld_relaxed(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -105,7 +125,7 @@ __device__ __forceinline__ uint32_t ld_relaxed(const uint32_t* p) {
 
 // Trace stamps (100 MHz constant clock) of the task being run, written by thread 0 when a trace
 // buffer is given: start, dependencies satisfied ("ready"), end.
-__device__ __forceinline__ void trace_stamp(const MegaParams& p, int task, int slot) {
+__device__ __forceinline__ void trace_stamp(MPc& p, int task, int slot) {
   if (p.trace != nullptr && threadIdx.x == 0) {
     uint64_t* rec = p.trace + 4 * (size_t)task;
     if (slot == 1) rec[0] = (uint64_t)task | ((uint64_t)blockIdx.x << 32);
@@ -113,7 +133,7 @@ __device__ __forceinline__ void trace_stamp(const MegaParams& p, int task, int s
   }
 }
 
-__device__ __forceinline__ uint32_t* counter(const MegaParams& p, int layer, int kind, int rb,
+__device__ __forceinline__ uint32_t* counter(MPc& p, int layer, int kind, int rb,
                                              int sub = 0) {
   return p.cnt + (((size_t)layer * kNumCounters + kind) * p.nrb + rb) * kSub + sub;
 }
@@ -135,11 +155,13 @@ __device__ __forceinline__ void acquire_agent() {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-// Block-wide: wait until *c has reached `target` (mod 2^32), bounded.  Thread 0 polls and then
-// performs the agent-scope acquire (it invalidates this CU's L1 and the XCD's L2 copies of other
-// XCDs' data for the whole workgroup); the barrier orders every other wave's later loads after
-// it.
-__device__ void mk_wait(const MegaParams& p, const uint32_t* c, uint32_t target) {
+// Block-wide: wait until *c has reached `target` (mod 2^32), bounded.  Thread 0 polls (the
+// counter's device-scope load skips the L1); with agent-scope hand-offs (LOCAL false) it then
+// performs the acquire (it invalidates this CU's L1 and the XCD's L2 copies of other XCDs' data
+// for the whole workgroup), while XCD-local consumers read produced data with device-scope loads
+// instead.  The barrier orders every wave's later loads after the wait.
+template <bool LOCAL>
+__device__ void mk_wait(MPc& p, const uint32_t* c, uint32_t target) {
   if (threadIdx.x == 0) {
     uint32_t spins = 0;
     while ((int32_t)(ld_relaxed(c) - target) < 0) {
@@ -150,19 +172,21 @@ __device__ void mk_wait(const MegaParams& p, const uint32_t* c, uint32_t target)
       }
       __builtin_amdgcn_s_sleep(1);
     }
-    acquire_agent();
+    if constexpr (!LOCAL) acquire_agent();
   }
   __syncthreads();
 }
 
 // Block-wide: publish this block's writes and count one arrival on *c.  Every wave first waits
-// for its own stores to complete; after the barrier one agent-scope release (L2 write-back of
-// the XCD) covers them all, then the counter is bumped.
+// for its own stores to complete (they are then in the XCD's L2); with agent-scope hand-offs one
+// release after the barrier (L2 write-back of the XCD) covers them all; then the counter is
+// bumped.
+template <bool LOCAL>
 __device__ void mk_signal(uint32_t* c) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    release_agent();
+    if constexpr (!LOCAL) release_agent();
     __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -198,10 +222,11 @@ struct NoHook {
   __device__ void operator()() const {}
 };
 
-template <int G, bool OUT_LDS, typename Hook = NoHook>
+template <int G, bool OUT_LDS, int POLICY = kLoadDefault, typename Hook = NoHook,
+          typename Pre = NoHook>
 __device__ void mk_layernorm_block(const half* src, const half* gamma, const half* beta,
                                    const uint8_t* valid, int row0, int nrows, int D, half* dst,
-                                   Hook hook = Hook{}) {
+                                   Hook hook = Hook{}, Pre pre = Pre{}) {
   constexpr int RPP = 64 / G;                 // rows per wave pass
   constexpr int PASSES = kMB / (4 * RPP);     // passes per wave (4 waves cover the 64 rows)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -213,12 +238,17 @@ __device__ void mk_layernorm_block(const half* src, const half* gamma, const hal
     g = *(const half8*)(gamma + 8 * c);
     bb = *(const half8*)(beta + 8 * c);
   }
+  pre();  // e.g. the wait for the rows: the affine vectors are in flight meanwhile
   half8 v[PASSES];
+  const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(src + (size_t)row0 * D, (uint32_t)nrows * D * 2);
 #pragma unroll
   for (int i = 0; i < PASSES; ++i) {
     const int r = (i * 4 + wave) * RPP + lane / G;
     v[i] = half8{};
-    if (act && r < nrows) v[i] = *(const half8*)(src + (size_t)(row0 + r) * D + 8 * c);
+    if (act && r < nrows) {
+      if constexpr (POLICY == kLoadDefault) v[i] = *(const half8*)(src + (size_t)(row0 + r) * D + 8 * c);
+      else v[i] = __builtin_bit_cast(half8, load16<POLICY>(sr, (uint32_t)(r * D + 8 * c) * 2));
+    }
   }
   hook();  // issued after the row loads, so the reductions below do not wait for its loads
 #pragma unroll
@@ -252,15 +282,19 @@ __device__ void mk_layernorm_block(const half* src, const half* gamma, const hal
   }
 }
 
-template <bool OUT_LDS, typename Hook = NoHook>
+template <bool OUT_LDS, int POLICY = kLoadDefault, typename Hook = NoHook, typename Pre = NoHook>
 __device__ void mk_layernorm(const half* src, const half* gamma, const half* beta,
                              const uint8_t* valid, int row0, int nrows, int D, half* dst,
-                             Hook hook = Hook{}) {
+                             Hook hook = Hook{}, Pre pre = Pre{}) {
   const int nch = D >> 3;
-  if (nch <= 8) mk_layernorm_block<8, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst, hook);
-  else if (nch <= 16) mk_layernorm_block<16, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst, hook);
-  else if (nch <= 32) mk_layernorm_block<32, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst, hook);
-  else mk_layernorm_block<64, OUT_LDS>(src, gamma, beta, valid, row0, nrows, D, dst, hook);
+  if (nch <= 8)
+    mk_layernorm_block<8, OUT_LDS, POLICY>(src, gamma, beta, valid, row0, nrows, D, dst, hook, pre);
+  else if (nch <= 16)
+    mk_layernorm_block<16, OUT_LDS, POLICY>(src, gamma, beta, valid, row0, nrows, D, dst, hook, pre);
+  else if (nch <= 32)
+    mk_layernorm_block<32, OUT_LDS, POLICY>(src, gamma, beta, valid, row0, nrows, D, dst, hook, pre);
+  else
+    mk_layernorm_block<64, OUT_LDS, POLICY>(src, gamma, beta, valid, row0, nrows, D, dst, hook, pre);
 }
 
 // ---- 64 x 64 GEMM tile, K streamed through an LDS ring of K steps ----
@@ -277,6 +311,7 @@ __device__ __forceinline__ void mk_copy_w(const half* W, int ld, int n0, int k0,
   }
 }
 
+template <int POLICY>
 __device__ __forceinline__ void mk_copy_a(const half* A, int ld, int row0, int nrows, int k0,
                                           half* dst) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -284,7 +319,7 @@ __device__ __forceinline__ void mk_copy_a(const half* A, int ld, int row0, int n
   for (int i = 0; i < 2; ++i) {
     const int r = min((wave + 4 * i) * 8 + (lane >> 3), nrows - 1);  // clamped rows: never stored
     const int c = (lane & 7) ^ (lane >> 3);
-    lds_copy16(A + (size_t)(row0 + r) * ld + k0 + 8 * c, dst + (wave + 4 * i) * 8 * 64);
+    lds_copy16<POLICY>(A + (size_t)(row0 + r) * ld + k0 + 8 * c, dst + (wave + 4 * i) * 8 * 64);
   }
 }
 
@@ -319,7 +354,7 @@ __device__ __forceinline__ void mk_prefetch_w(const half* W, int ld, int n0, int
 // rows, computed from the K steps as they pass through LDS -- 4 lanes per row take a step's 64
 // values, whose (mean, M2) are merged into the running ones (Chan et al.) -- and left in
 // srow[row] = (mean, rstd), biased variance, eps 1e-5.  The ring is free when this returns.
-template <bool RESA, bool STATS>
+template <bool RESA, bool STATS, int POLICY = kLoadDefault>
 __device__ floatx16 mk_tile_core(const half* A, int lda, const half* W, int ldw, int n0, int k0,
                                  int nk, int row0, int nrows, half* lds, float2* srow) {
   static_assert(!(RESA && STATS), "statistics come from the streamed A operand");
@@ -330,7 +365,7 @@ __device__ floatx16 mk_tile_core(const half* A, int lda, const half* W, int ldw,
   const int sr = threadIdx.x >> 2, sq = threadIdx.x & 3;  // statistics: row, quarter of a step
   const int pro = min(nk, R::NS - 1);  // K steps whose W copies mk_prefetch_w issued
   if constexpr (!RESA) {
-    for (int s = 0; s < pro; ++s) mk_copy_a(A, lda, row0, nrows, k0 + s * 64, R::a(lds, s));
+    for (int s = 0; s < pro; ++s) mk_copy_a<POLICY>(A, lda, row0, nrows, k0 + s * 64, R::a(lds, s));
   }
   floatx16 acc;
 #pragma unroll
@@ -394,7 +429,7 @@ __device__ floatx16 mk_tile_core(const half* A, int lda, const half* W, int ldw,
     const int nxt = kt + R::NS - 1;
     if (nxt < nk) {
       mk_copy_w(W, ldw, n0, k0 + nxt * 64, R::w(lds, nxt));
-      if constexpr (!RESA) mk_copy_a(A, lda, row0, nrows, k0 + nxt * 64, R::a(lds, nxt));
+      if constexpr (!RESA) mk_copy_a<POLICY>(A, lda, row0, nrows, k0 + nxt * 64, R::a(lds, nxt));
     }
     step(kt);
   }
@@ -446,15 +481,24 @@ __device__ __forceinline__ void mk_load_bias(TileCols& c, const half* bias, int 
 }
 
 // Residual of this lane's row and 16 columns and the row's mask bit.
+template <int POLICY = kLoadDefault>
 __device__ __forceinline__ void mk_load_resid(TileCols& c, const EpiArgs& ep, int row0, int nrows,
                                               int n0) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int mrow = row0 + min(wm * 32 + (lane & 31), nrows - 1);
-  c.ok = ep.valid == nullptr || ep.valid[mrow] != 0;
+  const int ml = min(wm * 32 + (lane & 31), nrows - 1);
+  c.ok = ep.valid == nullptr || ep.valid[row0 + ml] != 0;
+  const __amdgpu_buffer_rsrc_t rr =
+      buffer_rsrc(ep.resid + (size_t)row0 * ep.ldy, (uint32_t)nrows * ep.ldy * 2);
 #pragma unroll
-  for (int g = 0; g < 4; ++g)
-    c.res[g] = *(const half4*)(ep.resid + (size_t)mrow * ep.ldy + n0 + wn * 32 + 8 * g + 4 * (lane >> 5));
+  for (int g = 0; g < 4; ++g) {
+    const int col = n0 + wn * 32 + 8 * g + 4 * (lane >> 5);
+    if constexpr (POLICY == kLoadDefault)
+      c.res[g] = *(const half4*)(ep.resid + (size_t)(row0 + ml) * ep.ldy + col);
+    else
+      c.res[g] = __builtin_bit_cast(
+          half4, __builtin_amdgcn_raw_buffer_load_b64(rr, (uint32_t)(ml * ep.ldy + col) * 2, 0, POLICY));
+  }
 }
 
 template <int MODE>
@@ -555,7 +599,7 @@ __device__ void mk_gemm_tile(const half* A, const half* W, int K, int row0, int 
 }
 
 // kv_end (1 + last valid key) and prefix flag of sequence b, computed by the block.
-__device__ void mk_mask_summary(const MegaParams& p, int b, int* sred, int& kv_end, bool& prefix) {
+__device__ void mk_mask_summary(MPc& p, int b, int* sred, int& kv_end, bool& prefix) {
   if (p.mask == nullptr) {
     kv_end = p.S;
     prefix = true;
@@ -616,8 +660,14 @@ __global__ __launch_bounds__(kMKThreads) void ln_tile_kernel(LnTileArgs a) {
   mk_gemm_tile<MODE, true>(nullptr, a.w, a.D, row0, nrows, n0, a.ep, lds);
 }
 
-template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
+template <int HD, bool CAUSAL, bool LOCAL>
+__global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams) {
+  MPc* const pk = (MPc*)__builtin_amdgcn_kernarg_segment_ptr();
+  MPc& p = *pk;
+  // Loads of data written in this launch by other workgroups: with the XCD-local hand-off they
+  // bypass the CU's L1 (served by the XCD's L2); with the agent-scope hand-off the acquire has
+  // already invalidated the L1.
+  constexpr int PS = LOCAL ? kLoadDevice : kLoadDefault;
   extern __shared__ __align__(16) half lds[];
   half* sk = lds;                     // attention tiles reuse the start of the map
   half* sv = lds + 2 * kBKV * HD;
@@ -628,69 +678,109 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
   const AttnArgs aa{p.q, p.k, p.vt, p.mask, p.ctx, p.B, p.S, p.H, p.scale_log2};
   const int ksw = 64 * p.ksteps;                   // columns of h per FF2 split
 
-  for (int t = blockIdx.x; t < p.ntask; t += gridDim.x) {
-    trace_stamp(p, t, 1);
-    if (t >= p.L * p.per_layer) {  // FIN(rb)
-      const int rb = t - p.L * p.per_layer, b = rb / p.nsb, sb = rb - b * p.nsb;
+  // This workgroup's task list.  Agent-scope plan: the whole list, task t to workgroup t mod G.
+  // XCD-local plan: sequence b belongs to XCD b mod nx.  A workgroup reads the XCD it runs on
+  // from the hardware and draws a rank there from that XCD's ticket counter (the grid is nx W
+  // workgroups and dispatch deals them round-robin over the XCDs, from whichever XCD it starts
+  // at, so every XCD receives W of them); the W workgroups of an XCD take turns over the tasks
+  // of its sequences in list order.  A rank outside [0, W) (a dispatch that is not even) is
+  // recorded as an error: that workgroup runs no task, and the waits of the others give up.
+  int x0 = 0, dstep = 1, rank = blockIdx.x, nw = gridDim.x;
+  if constexpr (LOCAL) {
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    x0 = (int)(xcc & 0xF) % p.nx;
+    dstep = p.nx;
+    nw = gridDim.x / p.nx;
+    if (threadIdx.x == 0) {
+      const uint32_t ticket = __hip_atomic_fetch_add(p.ctrl + 8 + x0, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t r = ticket - (epoch - 1u) * (uint32_t)nw;
+      sred[8] = r < (uint32_t)nw ? (int)r : -1;
+      if (r >= (uint32_t)nw)
+        __hip_atomic_store(p.ctrl + 2, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    rank = sred[8];
+    __syncthreads();
+  }
+  const int nd = (x0 < p.B && rank >= 0) ? (p.B - 1 - x0) / dstep + 1 : 0;  // sequences in the list
+  // Tasks per sequence and layer of each kind (QKV, ATT, OUT, FF1, FF2), and the first index of
+  // each kind in a layer of the full list.
+  const int cnt[5] = {p.nsb * p.tq, p.H * p.nqb, p.nsb * p.td, p.nsb * p.tf, p.nsb * p.td * p.ks};
+  const int pdl = cnt[0] + cnt[1] + cnt[2] + cnt[3] + cnt[4];
+  const int nlayer = p.L * nd * pdl;
+
+  for (int v = rank; v < nlayer + nd * p.nsb; v += nw) {
+    MPc* pt = pk;
+    asm volatile("" : "+s"(pt));
+    MPc& p = *pt;
+    if (v >= nlayer) {  // FIN(rb)
+      const int i = v - nlayer, j = i / p.nsb, sb = i - j * p.nsb;
+      const int b = x0 + dstep * j, rb = b * p.nsb + sb;
+      const int t = p.L * p.per_layer + rb;
+      trace_stamp(p, t, 1);
       const int row0 = b * p.S + sb * kMB, nrows = min(kMB, p.S - sb * kMB);
-      mk_wait(p, counter(p, p.L - 1, cFF2, rb), epoch * (uint32_t)p.td);
-      trace_stamp(p, t, 2);
-      {
-        const int64_t dpad = (p.D + 63) / 64 * 64;
-        mk_layernorm<false>(p.xa, p.w + p.final_off, p.w + p.final_off + dpad, p.mask, row0, nrows,
-                            p.D, p.y);
-      }
-      __syncthreads();
+      const int64_t dpad = (p.D + 63) / 64 * 64;
+      mk_layernorm<false, PS>(p.xa, p.w + p.final_off, p.w + p.final_off + dpad, p.mask, row0,
+                              nrows, p.D, p.y, NoHook{}, [&] {
+                                mk_wait<LOCAL>(p, counter(p, p.L - 1, cFF2, rb), epoch * (uint32_t)p.td);
+                                trace_stamp(p, t, 2);
+                              });
       trace_stamp(p, t, 3);
       continue;
     }
-    // ---- decode task t
-    const int l = t / p.per_layer;
-    int i0 = t - l * p.per_layer;
-    int kind = 0;
-    {
-      const int seg[5] = {p.nrb * p.tq, p.B * p.H * p.nqb, p.nrb * p.td, p.nrb * p.tf,
-                          p.nrb * p.td * p.ks};
-      while (kind < 4 && i0 >= seg[kind]) i0 -= seg[kind++];
+    // ---- decode: layer l, kind, sequence b, index i1 within the sequence's tasks of that kind
+    const int l = v / (nd * pdl);
+    int i0 = v - l * nd * pdl;
+    int kind = 0, first = 0;
+    while (kind < 4 && i0 >= nd * cnt[kind]) {
+      i0 -= nd * cnt[kind];
+      first += p.B * cnt[kind];
+      ++kind;
     }
+    const int j = i0 / cnt[kind], i1 = i0 - j * cnt[kind];
+    const int b = x0 + dstep * j;
+    const int t = l * p.per_layer + first + b * cnt[kind] + i1;  // number in the full list
+    trace_stamp(p, t, 1);
     const half* wl = p.w + (size_t)l * p.stride;
 
     if (kind == 1) {  // ATT(l, b, h, qb): heaviest query blocks first when causal
-      const int bh = i0 / p.nqb;
-      int qb = i0 - bh * p.nqb;
+      const int h = i1 / p.nqb;
+      int qb = i1 - h * p.nqb;
       if (CAUSAL) qb = p.nqb - 1 - qb;
-      const int b = bh / p.H;
+      const int bh = b * p.H + h;
       int kv_end;
       bool prefix;
       mk_mask_summary(p, b, sred, kv_end, prefix);
       const int q_hi = min(p.S, (qb + 1) * kQB);
       const int key_hi = CAUSAL ? min(kv_end, q_hi) : kv_end;
       const int need = (max(key_hi, q_hi) + kMB - 1) / kMB;  // row blocks of keys and queries
-      for (int j = 0; j < need; ++j)
-        mk_wait(p, counter(p, l, cQKV, b * p.nsb + j), epoch * (uint32_t)p.tq);
+      for (int jj = 0; jj < need; ++jj)
+        mk_wait<LOCAL>(p, counter(p, l, cQKV, b * p.nsb + jj), epoch * (uint32_t)p.tq);
       trace_stamp(p, t, 2);
-      attention_block<HD, CAUSAL>(aa, bh, qb, kv_end, prefix, sk, sv);
+      attention_block<HD, CAUSAL, PS>(aa, bh, qb, kv_end, prefix, sk, sv);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       if (threadIdx.x == 0) {
-        release_agent();
-        for (int j = 2 * qb; j < min(2 * qb + 2, p.nsb); ++j)
-          __hip_atomic_fetch_add(counter(p, l, cATT, b * p.nsb + j), 1u, __ATOMIC_RELAXED,
+        if constexpr (!LOCAL) release_agent();
+        for (int jj = 2 * qb; jj < min(2 * qb + 2, p.nsb); ++jj)
+          __hip_atomic_fetch_add(counter(p, l, cATT, b * p.nsb + jj), 1u, __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
       }
       trace_stamp(p, t, 3);
       continue;
     }
 
-    // GEMM tasks: i0 = (rb * tiles + nt) (* ks + split for FF2)
-    int split = 0;
+    // GEMM tasks: i1 = (sb * tiles + nt) (* ks + split for FF2)
+    int split = 0, ii = i1;
     if (kind == 4) {
-      split = i0 % p.ks;
-      i0 /= p.ks;
+      split = ii % p.ks;
+      ii /= p.ks;
     }
     const int tiles = (kind == 0) ? p.tq : (kind == 3) ? p.tf : p.td;
-    const int rb = i0 / tiles, nt = i0 - rb * tiles;
-    const int b = rb / p.nsb, sb = rb - b * p.nsb;
+    const int sb = ii / tiles, nt = ii - sb * tiles;
+    const int rb = b * p.nsb + sb;
     const int row0 = b * p.S + sb * kMB, nrows = min(kMB, p.S - sb * kMB);
     const int n0 = nt * kNB;
     const int nkd = p.D / 64;
@@ -700,14 +790,14 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
       mk_prefetch_w<false>(W, p.D, n0, 0, nkd, lds);
       const FoldCols f = mk_load_fold((const float*)(wl + p.off[13]), (const float*)(wl + p.off[14]), n0);
       if (l > 0) {
-        mk_wait(p, counter(p, l - 1, cFF2, rb), epoch * (uint32_t)p.td);
+        mk_wait<LOCAL>(p, counter(p, l - 1, cFF2, rb), epoch * (uint32_t)p.td);
         // write-after-read on Q/K/V^T: attention of layer l-1 reading rows rb is done
-        for (int j = CAUSAL ? (sb & ~1) : 0; j < p.nsb; j += 2)
-          mk_wait(p, counter(p, l - 1, cATT, b * p.nsb + j), epoch * (uint32_t)p.H);
+        for (int jj = CAUSAL ? (sb & ~1) : 0; jj < p.nsb; jj += 2)
+          mk_wait<LOCAL>(p, counter(p, l - 1, cATT, b * p.nsb + jj), epoch * (uint32_t)p.H);
       }
       trace_stamp(p, t, 2);
-      const floatx16 acc = mk_tile_core<false, true>(l == 0 ? p.x : p.xa, p.D, W, p.D, n0, 0, nkd,
-                                                     row0, nrows, lds, srow);
+      const floatx16 acc = mk_tile_core<false, true, PS>(l == 0 ? p.x : p.xa, p.D, W, p.D, n0, 0,
+                                                         nkd, row0, nrows, lds, srow);
       ep.y = p.q;
       ep.ldy = 3 * p.D;
       ep.batch = p.B;
@@ -716,35 +806,35 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
       ep.head_dim = HD;
       ep.d_model = p.D;
       mk_epilogue_fold<TT_EPI_QKV>(acc, f, srow, ep, row0, nrows, n0);
-      mk_signal(counter(p, l, cQKV, rb));
+      mk_signal<LOCAL>(counter(p, l, cQKV, rb));
     } else if (kind == 2) {  // OUT
       const half* W = wl + p.off[4];
       mk_prefetch_w<false>(W, p.D, n0, 0, nkd, lds);
       TileCols c;
       mk_load_bias(c, wl + p.off[5], n0);
-      mk_wait(p, counter(p, l, cATT, rb), epoch * (uint32_t)p.H);
+      mk_wait<LOCAL>(p, counter(p, l, cATT, rb), epoch * (uint32_t)p.H);
       trace_stamp(p, t, 2);
       ep.resid = (l == 0) ? p.x : p.xa;
       ep.valid = p.mask;
       ep.y = p.xa;
       ep.ldy = p.D;
-      mk_load_resid(c, ep, row0, nrows, n0);
+      mk_load_resid<PS>(c, ep, row0, nrows, n0);
       const floatx16 acc =
-          mk_tile_core<false, false>(p.ctx, p.D, W, p.D, n0, 0, nkd, row0, nrows, lds, nullptr);
+          mk_tile_core<false, false, PS>(p.ctx, p.D, W, p.D, n0, 0, nkd, row0, nrows, lds, nullptr);
       mk_epilogue<TT_EPI_RESID_MASKED>(acc, c, ep, row0, nrows, n0);
-      mk_signal(counter(p, l, cOUT, rb));
+      mk_signal<LOCAL>(counter(p, l, cOUT, rb));
     } else if (kind == 3) {  // FF1: LayerNorm 2 folded into W'
       const half* W = wl + p.off[15];
       mk_prefetch_w<false>(W, p.D, n0, 0, nkd, lds);
       const FoldCols f = mk_load_fold((const float*)(wl + p.off[16]), (const float*)(wl + p.off[17]), n0);
-      mk_wait(p, counter(p, l, cOUT, rb), epoch * (uint32_t)p.td);
+      mk_wait<LOCAL>(p, counter(p, l, cOUT, rb), epoch * (uint32_t)p.td);
       trace_stamp(p, t, 2);
       const floatx16 acc =
-          mk_tile_core<false, true>(p.xa, p.D, W, p.D, n0, 0, nkd, row0, nrows, lds, srow);
+          mk_tile_core<false, true, PS>(p.xa, p.D, W, p.D, n0, 0, nkd, row0, nrows, lds, srow);
       ep.y = p.hbuf;
       ep.ldy = p.F;
       mk_epilogue_fold<TT_EPI_BIAS_GELU>(acc, f, srow, ep, row0, nrows, n0);
-      mk_signal(counter(p, l, cFF1, rb, nt / p.ksteps));
+      mk_signal<LOCAL>(counter(p, l, cFF1, rb, nt / p.ksteps));
     } else {  // FF2 split `split`: columns [split ksw, (split + 1) ksw) of h and W2
       const half* W = wl + p.off[10];
       const int k0 = split * ksw;
@@ -752,15 +842,15 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
       mk_prefetch_w<false>(W, p.F, n0, k0, p.ksteps, lds);
       TileCols c;
       if (reducer) mk_load_bias(c, wl + p.off[11], n0);
-      mk_wait(p, counter(p, l, cFF1, rb, split), epoch * (uint32_t)p.ksteps);
+      mk_wait<LOCAL>(p, counter(p, l, cFF1, rb, split), epoch * (uint32_t)p.ksteps);
       trace_stamp(p, t, 2);
       ep.resid = p.xa;
       ep.valid = p.mask;
       ep.y = p.xa;
       ep.ldy = p.D;
-      if (reducer) mk_load_resid(c, ep, row0, nrows, n0);
-      floatx16 acc =
-          mk_tile_core<false, false>(p.hbuf, p.F, W, p.F, n0, k0, p.ksteps, row0, nrows, lds, nullptr);
+      if (reducer) mk_load_resid<PS>(c, ep, row0, nrows, n0);
+      floatx16 acc = mk_tile_core<false, false, PS>(p.hbuf, p.F, W, p.F, n0, k0, p.ksteps, row0,
+                                                    nrows, lds, nullptr);
       // Split-K: splits 0 .. ks-2 store fp32 partial tiles (per lane, in accumulator order) and
       // count their arrival; the last split (numbered after them, so it may wait for them) adds
       // the partials and its own accumulator in split order and runs the epilogue.
@@ -770,19 +860,22 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
 #pragma unroll
         for (int g = 0; g < 4; ++g)
           mine[g] = floatx4{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
-        mk_signal(counter(p, l, cFF2T, rb, nt));
+        mk_signal<LOCAL>(counter(p, l, cFF2T, rb, nt));
         trace_stamp(p, t, 3);
         continue;
       }
       if (p.ks > 1) {
-        mk_wait(p, counter(p, l, cFF2T, rb, nt), epoch * (uint32_t)(p.ks - 1));
+        mk_wait<LOCAL>(p, counter(p, l, cFF2T, rb, nt), epoch * (uint32_t)(p.ks - 1));
+        const __amdgpu_buffer_rsrc_t pr = buffer_rsrc(part, (uint32_t)(p.ks - 1) * kMKThreads * 64);
         floatx4 sum[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) sum[g] = floatx4{0.f, 0.f, 0.f, 0.f};
-        for (int j = 0; j < p.ks - 1; ++j) {
-          const floatx4* src = (const floatx4*)(part + (size_t)j * (kMKThreads * 16)) + 4 * threadIdx.x;
+        for (int s2 = 0; s2 < p.ks - 1; ++s2) {
 #pragma unroll
-          for (int g = 0; g < 4; ++g) sum[g] += src[g];
+          for (int g = 0; g < 4; ++g) {
+            const uint32_t off = ((uint32_t)s2 * kMKThreads * 16 + (4 * threadIdx.x + g) * 4) * 4;
+            sum[g] += __builtin_bit_cast(floatx4, load16<PS>(pr, off));
+          }
         }
 #pragma unroll
         for (int g = 0; g < 4; ++g)
@@ -790,7 +883,7 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams p) {
           for (int e = 0; e < 4; ++e) acc[4 * g + e] = sum[g][e] + acc[4 * g + e];
       }
       mk_epilogue<TT_EPI_MASKED_RESID>(acc, c, ep, row0, nrows, n0);
-      mk_signal(counter(p, l, cFF2, rb));
+      mk_signal<LOCAL>(counter(p, l, cFF2, rb));
     }
     trace_stamp(p, t, 3);
   }
@@ -885,29 +978,35 @@ int megakernel_supported(int B, int S, int D, int H, int F, int L) {
   return TT_OK;
 }
 
-template <int HD, bool CAUSAL>
-static int launch_mega(MegaParams& p, hipStream_t stream) {
+template <int HD, bool CAUSAL, bool LOCAL>
+static int launch_mega(MegaParams& p, int cus, hipStream_t stream) {
   const size_t lds = kLdsHalfs * sizeof(half) + 64 + 64 * sizeof(float2);
   static_assert(2 * kBKV * HD * 2 <= kLdsHalfs, "attention tiles must fit the LDS map");
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   static int per_cu = 0;
   std::call_once(once, [&] {
-    attr = hipFuncSetAttribute((const void*)megakernel<HD, CAUSAL>,
+    attr = hipFuncSetAttribute((const void*)megakernel<HD, CAUSAL, LOCAL>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr == hipSuccess)
-      attr = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, megakernel<HD, CAUSAL>,
+      attr = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, megakernel<HD, CAUSAL, LOCAL>,
                                                           kMKThreads, lds);
   });
   if (attr != hipSuccess) return fail(TT_ERR_HIP, "megakernel setup: %s", hipGetErrorString(attr));
-  int dev = 0, cus = 0;
-  TT_HIP(hipGetDevice(&dev));
-  TT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-  // One workgroup per task up to one per CU (all resident): with few tasks every workgroup
-  // prefetches its weights at once, with many each runs a task of every stage in turn.
   if (per_cu < 1) return fail(TT_ERR_HIP, "megakernel: a workgroup does not fit a CU");
-  const int grid = std::max(1, std::min(p.ntask, cus));
-  hipLaunchKernelGGL((megakernel<HD, CAUSAL>), dim3(grid), dim3(kMKThreads), lds, stream, p);
+  // One workgroup per task up to one per CU (all resident): with few tasks every workgroup
+  // prefetches its weights at once, with many each runs a task of every stage in turn.  The
+  // XCD-local plan sizes this per XCD (its first XCD holds the most sequences) and launches the
+  // same number on every XCD, so that round-robin dispatch puts workgroup g on XCD g mod nx.
+  int grid;
+  if (LOCAL) {
+    const int nd = (p.B + p.nx - 1) / p.nx;
+    const int per_xcd = p.L * nd * (p.per_layer / p.B) + nd * p.nsb;
+    grid = p.nx * std::max(1, std::min(per_xcd, cus / p.nx));
+  } else {
+    grid = std::max(1, std::min(p.ntask, cus));
+  }
+  hipLaunchKernelGGL((megakernel<HD, CAUSAL, LOCAL>), dim3(grid), dim3(kMKThreads), lds, stream, p);
   return launch_status("megakernel");
 }
 
@@ -957,9 +1056,16 @@ size_t megakernel_error_offset(int B, int S, int D, int F, int L) {
 
 static uint32_t g_spin_limit = kSpinLimit;
 
+
 void megakernel_set_spin_limit(int64_t limit) {
   g_spin_limit = limit < 0 ? kSpinLimit : (uint32_t)std::min<int64_t>(limit, 0xFFFFFFFFll);
 }
+
+constexpr int kMaxDevices = 64;
+struct DevInfo {
+  int cus = 0, nx = 1;
+  bool xcds_known = false, valid = false;
+};
 
 int launch_megakernel(const half* weights, const int64_t off[TT_LAYER_SEGMENTS], int64_t stride,
                       int64_t final_off,
@@ -1008,9 +1114,40 @@ int launch_megakernel(const half* weights, const int64_t off[TT_LAYER_SEGMENTS],
   p.per_layer = p.nrb * p.tq + B * H * p.nqb + p.nrb * p.td + p.nrb * p.tf + p.nrb * p.td * p.ks;
   p.ntask = L * p.per_layer + p.nrb;
   p.scale_log2 = (1.0f / sqrtf((float)(D / H))) * 1.4426950408889634f;
+  int dev = 0;
+  TT_HIP(hipGetDevice(&dev));
+  TT_REQUIRE(dev >= 0 && dev < kMaxDevices, "megakernel: device %d", dev);
+  // Device attributes, queried once per device (a forward of the small shapes this plan serves
+  // lasts about as long as a few attribute queries).  The XCD-local hand-off needs the XCD count
+  // (every XCD gets the same number of workgroups); without it the agent-scope plan runs.
+  static std::mutex mu;
+  static DevInfo info[kMaxDevices];
+  DevInfo di;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    if (!info[dev].valid) {
+      int cus = 0, nx = 0;
+      TT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+      info[dev].cus = cus;
+      info[dev].xcds_known = hipDeviceGetAttribute(&nx, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess &&
+                             nx >= 1 && nx <= 8 && cus % nx == 0;
+      info[dev].nx = info[dev].xcds_known ? nx : 1;
+      info[dev].valid = true;
+    }
+    di = info[dev];
+  }
+  const int cus = di.cus;
+  const bool xcds_known = di.xcds_known;
+  p.nx = di.nx;
   const int hd = D / H;
-  if (hd == 64) return causal ? launch_mega<64, true>(p, stream) : launch_mega<64, false>(p, stream);
-  return causal ? launch_mega<32, true>(p, stream) : launch_mega<32, false>(p, stream);
+  if (xcds_known) {
+    if (hd == 64)
+      return causal ? launch_mega<64, true, true>(p, cus, stream) : launch_mega<64, false, true>(p, cus, stream);
+    return causal ? launch_mega<32, true, true>(p, cus, stream) : launch_mega<32, false, true>(p, cus, stream);
+  }
+  if (hd == 64)
+    return causal ? launch_mega<64, true, false>(p, cus, stream) : launch_mega<64, false, false>(p, cus, stream);
+  return causal ? launch_mega<32, true, false>(p, cus, stream) : launch_mega<32, false, false>(p, cus, stream);
 }
 
 __global__ void mk_zero_words(uint32_t* __restrict__ p, size_t n) {
