@@ -2,8 +2,9 @@
 // attention kernel and the persistent megakernel).
 //
 // One 256-thread block owns (sequence b, head h, 128-query tile); each of its four waves owns 32
-// queries.  Key/value tiles of 64 keys are staged in LDS (double-buffered) by
-// global_load_lds_dwordx4 copies issued one tile ahead, so no registers hold in-flight tiles.
+// queries.  Key/value tiles of 64 keys are staged in LDS (double-buffered) by buffer -> LDS
+// dwordx4 copies issued one tile ahead, so no registers hold in-flight tiles; each lane's source
+// offset is fixed and the tile start moves the wave-uniform buffer base.
 // Per wave and tile:
 //   S^T = K Q^T   with v_mfma_f32_32x32x16_f16 (K from LDS as the A operand, Q^T held in
 //                 registers as the B operand), so lane l holds one query (l % 32) and 32 of the 64
@@ -12,11 +13,13 @@
 // To make the probabilities a lane already holds line up with 8 consecutive keys of V^T, K rows
 // are placed in LDS with bits 2 and 3 of the row index swapped: S^T row r then holds key pi(r),
 // and lane l of key block kb holds keys 32kb + 16(j/8) + 8(l/32) + (j%8), j = 0..15.
-// Softmax runs in the exp2 domain with scale*log2(e) folded into one FMA per score.  The running
-// max is refreshed lazily: the output is rescaled only when some row's max grows by more than
-// 2^8 over the reference max in use (exp2 of a score minus a stale reference is then at most 256,
-// exact in fp32 and in the fp16 probabilities).  Row sums add the fp16 probabilities that feed
-// the P V MFMA (v_dot2_f32_f16), so numerator and denominator use the same rounded values.
+// Softmax runs in the exp2 domain: Q is multiplied by scale*log2(e) when it is loaded, and the
+// S^T MFMA chains start from minus the row's reference max instead of zero, so each score leaves
+// the MFMA ready for v_exp_f32.  The reference max is refreshed lazily: the output is rescaled
+// only when some row's max grows by more than 2^8 over the reference in use (exp2 of a score
+// minus a stale reference is then at most 256, exact in fp32 and in the fp16 probabilities).
+// Row sums add the fp16 probabilities that feed the P V MFMA (v_dot2_f32_f16), so numerator and
+// denominator use the same rounded values.
 // Masking: keys are dropped when key >= kv_end (last valid key + 1), when causal && key > query,
 // and, for masks that are not right-padded prefixes, when mask[b, key] == 0.  Query rows that are
 // padded are written as +0.0.  Causal query tiles are scheduled heaviest-first.
@@ -103,7 +106,8 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
   const int S = a.S, H = a.H;
   const float scale_log2 = a.scale_log2;
   const int b = bh / H, h = bh - b * H;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hf = lane >> 5, col = lane & 31;
   const int ldv = round_up(S, kBKV);
 
@@ -126,27 +130,29 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
   // rows p = (wave * KCOPIES + c) * KRPC + lane / KCH with key pi(p) at logical chunk
   // (lane % KCH) ^ swizzle(p); V^T copy c fills row d = (wave * VCOPIES + c) * 8 + lane / 8 with
   // keys 8 ((lane % 8) ^ (d % 8)) .. +7 of feature row d.
-  int krow[KCOPIES], koff[KCOPIES], voff[VCOPIES];
+  // Key rows at or past S lie outside the K buffer's range, so those lanes read no memory (their
+  // LDS rows hold whatever the buffer check leaves there); the scores of such keys are always
+  // masked, by selection, so no value of those rows can reach the output.
+  uint32_t koff[KCOPIES], voff[VCOPIES];
 #pragma unroll
   for (int c = 0; c < KCOPIES; ++c) {
     const int p = (wave * KCOPIES + c) * KRPC + lane / KCH;
-    krow[c] = (p & ~31) | pi23(p & 31);
-    koff[c] = kswz<HD>(p, lane % KCH) * 8;
+    koff[c] = (uint32_t)(((p & ~31) | pi23(p & 31)) * HD + kswz<HD>(p, lane % KCH) * 8) * 2;
   }
 #pragma unroll
   for (int c = 0; c < VCOPIES; ++c) {
     const int d = (wave * VCOPIES + c) * 8 + (lane >> 3);
-    voff[c] = d * ldv + vswz(d, lane & 7) * 8;
+    voff[c] = (uint32_t)(d * ldv + vswz(d, lane & 7) * 8) * 2;
   }
   auto issue_tile = [&](int t0, int st) {
+    const __amdgpu_buffer_rsrc_t kr = buffer_rsrc(Kbh + (size_t)t0 * HD, (uint32_t)(S - t0) * HD * 2);
 #pragma unroll
-    for (int c = 0; c < KCOPIES; ++c) {
-      const int key = min(t0 + krow[c], S - 1);  // rows past S load valid memory, never used
-      lds_copy16<POLICY>(Kbh + (size_t)key * HD + koff[c], &sk[st][(wave * KCOPIES + c) * 512]);
-    }
+    for (int c = 0; c < KCOPIES; ++c)
+      lds_copy16_buf<POLICY>(kr, koff[c], &sk[st][(wave * KCOPIES + c) * 512]);
+    const __amdgpu_buffer_rsrc_t vr = buffer_rsrc(Vbh + t0, (uint32_t)(HD * ldv - t0) * 2);
 #pragma unroll
     for (int c = 0; c < VCOPIES; ++c)
-      lds_copy16<POLICY>(Vbh + voff[c] + t0, &sv[st][(wave * VCOPIES + c) * 512]);
+      lds_copy16_buf<POLICY>(vr, voff[c], &sv[st][(wave * VCOPIES + c) * 512]);
   };
   // V^T columns of keys >= S (padding of the last, partial tile) are cleared in LDS so that
   // 0-probability keys contribute 0 * 0, whatever the padding memory holds.
@@ -158,6 +164,8 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     }
   };
 
+  // Q is held pre-multiplied by scale * log2(e) (rounded to fp16 once), so the MFMA yields
+  // scores in the log2 domain directly.
   half8 qf[KSTEPS];
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) {
@@ -168,6 +176,8 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         const __amdgpu_buffer_rsrc_t qr = buffer_rsrc(Qbh, (uint32_t)S * HD * 2);
         qf[kk] = __builtin_bit_cast(half8, load16<POLICY>(qr, (uint32_t)(q * HD + 16 * kk + 8 * hf) * 2));
       }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[kk][e] = (half)((float)qf[kk][e] * scale_log2);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) qf[kk][e] = (half)0.f;
@@ -181,6 +191,13 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     for (int e = 0; e < 16; ++e) o[i][e] = 0.f;
   float m_ref = -INFINITY;  // reference max (log2 domain) the running sums are scaled to
   float l_run = 0.f;        // this lane's half of the row sum
+  // The S^T MFMA chains start from -m_ref (0 while no key of the row has been seen), so the
+  // scores come out relative to the reference max and exp2 applies to them directly.  thr is
+  // the relative tile max above which the reference moves.
+  float thr = -INFINITY;
+  floatx16 sinit;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) sinit[e] = 0.f;
 
   // Non-prefix masks: this lane's key-mask byte for the current and the next tile, loaded when
   // the tile's copies are issued so the end-of-tile wait covers it.
@@ -212,13 +229,11 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
       floatx16 s[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
         const int row = kb * 32 + col;
 #pragma unroll
         for (int kk = 0; kk < KSTEPS; ++kk) {
           const half8 a = *(const half8*)(&sk[st][row * HD + kswz<HD>(row, 2 * kk + hf) * 8]);
-          s[kb] = mfma32x32x16(a, qf[kk], s[kb]);
+          s[kb] = mfma32x32x16(a, qf[kk], kk == 0 ? sinit : s[kb]);
         }
       }
       const bool need_mask = (t0 + kBKV > kv_end) || (CAUSAL && t0 + kBKV - 1 > qw) || keymask;
@@ -250,28 +265,37 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[kb][j]);
-      const float mt = xhalf_max(mx) * scale_log2;  // tile row max, log2 domain
-      if (__builtin_amdgcn_ballot_w64(mt > m_ref + kLazy) != 0) {
+      const float mt = xhalf_max(mx);  // tile row max relative to the reference in use
+      if (__builtin_amdgcn_ballot_w64(mt > thr) != 0) {
         // Rescale: the new reference is the true running max (lanes whose max did not grow
-        // get corr = 1).  A row with no valid key so far keeps m_ref = -inf and o = l = 0.
-        const float m_new = fmaxf(m_ref, mt);
+        // get corr = 1 and shift 0).  A row with no valid key so far keeps m_ref = -inf and
+        // o = l = 0.
+        const float mc = (m_ref == -INFINITY) ? 0.f : m_ref;  // offset the scores carry
+        const float m_new = fmaxf(m_ref, mt + mc);
         const float corr = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+        const float shift = (m_new == -INFINITY) ? 0.f : m_new - mc;
         m_ref = m_new;
+        thr = (m_new == -INFINITY) ? -INFINITY : kLazy;
         l_run *= corr;
 #pragma unroll
         for (int i = 0; i < DB; ++i)
 #pragma unroll
           for (int e = 0; e < 16; ++e) o[i][e] *= corr;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) s[kb][e] -= shift;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sinit[e] = (m_new == -INFINITY) ? 0.f : -m_new;
       }
-      const float mc = (m_ref == -INFINITY) ? 0.f : m_ref;
       half8 p16[2][2];
       const half2v ones = {(half)1.f, (half)1.f};
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int j = 0; j < 16; j += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kb][j], scale_log2, -mc));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kb][j + 1], scale_log2, -mc));
+          const float p0 = __builtin_amdgcn_exp2f(s[kb][j]);
+          const float p1 = __builtin_amdgcn_exp2f(s[kb][j + 1]);
           const half2v pp = {(half)p0, (half)p1};
           l_run = __builtin_amdgcn_fdot2(pp, ones, l_run, false);
           p16[kb][j >> 3][j & 7] = pp[0];

@@ -97,6 +97,15 @@ __device__ __forceinline__ void lds_copy16(const half* src, half* lds_dst) {
                                    (__attribute__((address_space(3))) void*)lds_dst, 16, 0, POLICY);
 }
 
+// 16 bytes per lane from byte offset `off` of the buffer `r` straight into LDS at lds_dst +
+// 16 * lane (lds_dst wave-uniform); lanes whose 16 bytes lie outside the buffer read nothing
+// from memory.
+template <int POLICY = kLoadDefault>
+__device__ __forceinline__ void lds_copy16_buf(__amdgpu_buffer_rsrc_t r, uint32_t off, half* lds_dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_dst, 16,
+                                           off, 0, 0, POLICY);
+}
+
 // Raw buffer resource over [base, base + bytes): stride 0; 0x00020000 is the data-format word
 // for untyped 32-bit accesses.  `base` must be wave-uniform.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
