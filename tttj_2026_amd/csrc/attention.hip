@@ -57,15 +57,19 @@ int attention_head_dim_supported(int head_dim) {
   return TT_OK;
 }
 
+float attention_q_scale(int head_dim) {
+  return (1.0f / sqrtf((float)head_dim)) * 1.4426950408889634f;
+}
+
 int launch_attention(const half* q, const half* k, const half* vt, const uint8_t* mask,
                      const int32_t* info, half* ctx, int batch, int seq, int heads, int head_dim,
-                     int causal, hipStream_t stream) {
+                     int causal, hipStream_t stream, bool q_prescaled) {
   TT_REQUIRE(batch > 0 && seq > 0 && heads > 0, "attention: bad shape");
   int rc = attention_head_dim_supported(head_dim);
   if (rc != TT_OK) return rc;
   TT_REQUIRE(mask == nullptr || info != nullptr, "attention: a mask needs its mask_info");
-  const float scale_log2 = (1.0f / sqrtf((float)head_dim)) * 1.4426950408889634f;
-  const AttnArgs args{q, k, vt, mask, ctx, batch, seq, heads, scale_log2};
+  const AttnArgs args{q, k, vt, mask, ctx, batch, seq, heads, attention_q_scale(head_dim),
+                      q_prescaled ? 1 : 0};
   if (head_dim <= 16) return launch_attention_small(args, info, head_dim, causal, stream);
   if (head_dim == 256) return launch_attention_wide(args, info, head_dim, causal, stream);
   switch (head_dim) {

@@ -13,9 +13,10 @@
 // To make the probabilities a lane already holds line up with 8 consecutive keys of V^T, K rows
 // are placed in LDS with bits 2 and 3 of the row index swapped: S^T row r then holds key pi(r),
 // and lane l of key block kb holds keys 32kb + 16(j/8) + 8(l/32) + (j%8), j = 0..15.
-// Softmax runs in the exp2 domain: Q is multiplied by scale*log2(e) when it is loaded, and the
-// S^T MFMA chains start from minus the row's reference max instead of zero, so each score leaves
-// the MFMA ready for v_exp_f32.  The reference max is refreshed lazily: the output is rescaled
+// Softmax runs in the exp2 domain: Q arrives multiplied by scale*log2(e) (from the forward's QKV
+// epilogue, with one fp16 rounding as unscaled Q would have; through the C ABI, multiplied and
+// rounded again when the block loads it), and the S^T MFMA chains start from minus the row's
+// reference max instead of zero, so each score leaves the MFMA ready for v_exp_f32.  The reference max is refreshed lazily: the output is rescaled
 // only when some row's max grows by more than 2^8 over the reference in use (exp2 of a score
 // minus a stale reference is then at most 256, exact in fp32 and in the fp16 probabilities).
 // Row sums add the fp16 probabilities that feed the P V MFMA (v_dot2_f32_f16), so numerator and
@@ -77,6 +78,9 @@ struct AttnArgs {
   half* ctx;           // [B, S, H * hd]
   int B, S, H;
   float scale_log2;    // hd^-1/2 * log2(e)
+  // Q already multiplied by scale_log2 (rounded to fp16 once, by the QKV projection's epilogue);
+  // otherwise the block multiplies and rounds it when it loads it.
+  int q_prescaled;
 };
 
 // One (sequence b, head h, 128-query tile qt) attention block on 256 threads.  kv_end is
@@ -164,8 +168,8 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     }
   };
 
-  // Q is held pre-multiplied by scale * log2(e) (rounded to fp16 once), so the MFMA yields
-  // scores in the log2 domain directly.
+  // Q is held multiplied by scale * log2(e) (in fp16), so the MFMA yields scores in the log2
+  // domain directly.
   half8 qf[KSTEPS];
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) {
@@ -176,8 +180,10 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         const __amdgpu_buffer_rsrc_t qr = buffer_rsrc(Qbh, (uint32_t)S * HD * 2);
         qf[kk] = __builtin_bit_cast(half8, load16<POLICY>(qr, (uint32_t)(q * HD + 16 * kk + 8 * hf) * 2));
       }
+      if (!a.q_prescaled) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qf[kk][e] = (half)((float)qf[kk][e] * scale_log2);
+        for (int e = 0; e < 8; ++e) qf[kk][e] = (half)((float)qf[kk][e] * scale_log2);
+      }
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) qf[kk][e] = (half)0.f;

@@ -49,7 +49,7 @@ __global__ __launch_bounds__(kSmallBQ) void attention_small_kernel(AttnArgs a,
   float qf[HD], o[HD];
 #pragma unroll
   for (int d = 0; d < HD; ++d) {
-    qf[d] = q < S ? (float)Qbh[(size_t)q * HD + d] * a.scale_log2 : 0.f;
+    qf[d] = q < S ? (float)Qbh[(size_t)q * HD + d] * (a.q_prescaled ? 1.f : a.scale_log2) : 0.f;
     o[d] = 0.f;
   }
   float m = -INFINITY, l = 0.f;

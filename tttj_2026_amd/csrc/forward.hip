@@ -295,6 +295,7 @@ int transformer_fwd(const void* weights, const void* x, const uint8_t* mask, voi
     ep.heads = H;
     ep.head_dim = hd;
     ep.d_model = D;
+    ep.q_scale = attention_q_scale(hd);  // Q leaves the projection in the attention's form
     if (fused_ln) {
       if ((rc = launch_ln_tile(cur, w + lay.off[0], w + lay.off[1], w + lay.off[2], ep, B, S, D,
                                3 * D, stream)) != TT_OK)
@@ -314,7 +315,8 @@ int transformer_fwd(const void* weights, const void* x, const uint8_t* mask, voi
       ep.ln_bias = (const float*)(w + lay.off[14]);
       if ((rc = launch_linear(cur, w + lay.off[12], T, 3 * D, D, ep, stream)) != TT_OK) return rc;
     }
-    if ((rc = launch_attention(q, k, vt, mask, info, ws.xn, B, S, H, hd, causal, stream)) != TT_OK)
+    if ((rc = launch_attention(q, k, vt, mask, info, ws.xn, B, S, H, hd, causal, stream, true)) !=
+        TT_OK)
       return rc;
     ep = EpiArgs{};
     ep.bias = w + lay.off[5];

@@ -413,6 +413,8 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1)
   }
   // Modes without a residual write masked rows as +0.0 (the residual modes handle the mask
   // when they store).
+  float qs = 1.f;  // Q columns of the QKV projection carry ep.q_scale
+  if constexpr (MODE == TT_EPI_QKV) qs = n0 < ep.d_model ? ep.q_scale : 1.f;
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
     const int ml = j * 32 + (lane & 31);
@@ -429,6 +431,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1)
         for (int e = 0; e < 4; ++e) {
           float v = acc[i][j][4 * g + e] + (float)bv[e];
           if constexpr (MODE == TT_EPI_BIAS_GELU) v = gelu_erf(v);
+          if constexpr (MODE == TT_EPI_QKV) v *= qs;
           h[e] = keep ? (half)v : (half)0.f;
         }
         if (vt_scalar) {
@@ -597,6 +600,7 @@ __device__ __forceinline__ void epilogue4(const EpiArgs& ep, int m, int n, const
     else
       v = acc[e] + (float)ep.bias[n + e];
     if constexpr (MODE == TT_EPI_BIAS_GELU) v = gelu_erf(v);
+    if constexpr (MODE == TT_EPI_QKV) v *= n < ep.d_model ? ep.q_scale : 1.f;
     hv[e] = (half)v;
   }
   if constexpr (MODE == TT_EPI_QKV) {

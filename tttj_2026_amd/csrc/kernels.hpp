@@ -13,6 +13,9 @@ struct EpiArgs {
   int ldy;
   int mode;              // TT_EPI_*
   int batch, seq, heads, head_dim, d_model;  // TT_EPI_QKV only
+  // TT_EPI_QKV: factor on the Q columns before their fp16 rounding.  The forward passes
+  // hd^-1/2 log2(e), the form its attention launches read Q in (AttnArgs::q_prescaled).
+  float q_scale = 1.f;
   // LayerNorm folded into this projection (TT_EPI_QKV / TT_EPI_BIAS_GELU, on the narrow and
   // small kernels): X is the raw residual stream, W = W diag(gamma), and the epilogue computes
   // rstd (acc - mean c) + b' instead of acc + bias.  The row statistics come from ln_slots
@@ -44,9 +47,13 @@ int launch_pack_derived(half* w, int64_t stride, const int64_t* off, int D, int 
 
 int launch_mask_info(const uint8_t* mask, int32_t* info, int batch, int seq, hipStream_t stream);
 
+// q_prescaled: q holds Q multiplied by attention_q_scale(head_dim) (the forward's QKV epilogue
+// writes it so, EpiArgs::q_scale); otherwise the kernels multiply it when they load it.
 int launch_attention(const half* q, const half* k, const half* vt, const uint8_t* mask,
                      const int32_t* info, half* ctx, int batch, int seq, int heads, int head_dim,
-                     int causal, hipStream_t stream);
+                     int causal, hipStream_t stream, bool q_prescaled = false);
+// hd^-1/2 log2(e): the factor of the scores in the exp2-domain softmax.
+float attention_q_scale(int head_dim);
 int attention_head_dim_supported(int head_dim);
 
 struct AttnArgs;

@@ -527,7 +527,8 @@ __device__ void mk_epilogue(const floatx16& acc, const TileCols& c, const EpiArg
     half4 h;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float v = acc[4 * g + e] + (float)c.bias[g][e];
+      float v = acc[4 * g + e] + (float)c.bias[g][e];
+      if constexpr (MODE == TT_EPI_QKV) v *= n < ep.d_model ? ep.q_scale : 1.f;
       if constexpr (MODE == TT_EPI_BIAS_GELU) {
         h[e] = (half)gelu_erf(v);
       } else if constexpr (RESID) {
@@ -581,6 +582,7 @@ __device__ void mk_epilogue_fold(const floatx16& acc, const FoldCols& f, const f
     for (int e = 0; e < 4; ++e) {
       float v = fmaf(rs.y, fmaf(-rs.x, f.c[g][e], acc[4 * g + e]), f.b[g][e]);
       if constexpr (MODE == TT_EPI_BIAS_GELU) v = gelu_erf(v);
+      if constexpr (MODE == TT_EPI_QKV) v *= n < ep.d_model ? ep.q_scale : 1.f;
       h[e] = (half)v;
     }
     mk_store4<MODE>(ep, m, n, h);
@@ -675,7 +677,8 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams) {
   float2* srow = (float2*)(lds + kLdsHalfs + 32);         // 64 (mean, rstd) pairs
 
   const uint32_t epoch = ld_relaxed(p.ctrl) + 1u;  // this launch's number (workspace starts at 0)
-  const AttnArgs aa{p.q, p.k, p.vt, p.mask, p.ctx, p.B, p.S, p.H, p.scale_log2};
+  // Q is written multiplied by scale_log2 (QKV task epilogue), the form attention_block reads
+  const AttnArgs aa{p.q, p.k, p.vt, p.mask, p.ctx, p.B, p.S, p.H, p.scale_log2, 1};
   const int ksw = 64 * p.ksteps;                   // columns of h per FF2 split
 
   // This workgroup's task list.  Agent-scope plan: the whole list, task t to workgroup t mod G.
@@ -805,6 +808,7 @@ __global__ __launch_bounds__(kMKThreads) void megakernel(MegaParams) {
       ep.heads = p.H;
       ep.head_dim = HD;
       ep.d_model = p.D;
+      ep.q_scale = p.scale_log2;
       mk_epilogue_fold<TT_EPI_QKV>(acc, f, srow, ep, row0, nrows, n0);
       mk_signal<LOCAL>(counter(p, l, cQKV, rb));
     } else if (kind == 2) {  // OUT
@@ -1113,7 +1117,7 @@ int launch_megakernel(const half* weights, const int64_t off[TT_LAYER_SEGMENTS],
   p.ksteps = F / 64 / p.ks;
   p.per_layer = p.nrb * p.tq + B * H * p.nqb + p.nrb * p.td + p.nrb * p.tf + p.nrb * p.td * p.ks;
   p.ntask = L * p.per_layer + p.nrb;
-  p.scale_log2 = (1.0f / sqrtf((float)(D / H))) * 1.4426950408889634f;
+  p.scale_log2 = attention_q_scale(D / H);
   int dev = 0;
   TT_HIP(hipGetDevice(&dev));
   TT_REQUIRE(dev >= 0 && dev < kMaxDevices, "megakernel: device %d", dev);
