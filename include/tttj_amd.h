@@ -196,6 +196,18 @@ int tt_attention_fwd(const void* q, const void* k, const void* vt, const uint8_t
                      const int32_t* info, void* ctx, int batch, int seq, int heads, int head_dim,
                      int causal, void* stream);
 
+/* Where a forward's intermediates of its LAST layer are left in the workspace, for per-stage checks
+ * of the fused plans (the megakernel's tasks and the fused-LN tiles never materialise LN1 / LN2 or
+ * the other stages on their own): byte offsets of the Q / K / V^T planes (the TT_EPI_QKV layout;
+ * Q is stored multiplied by hd^-1/2 log2(e), the form the attention kernels read), of the attention
+ * context [B,S,D] (-1 when the plan overwrites it with the LN2 output) and of the FFN hidden
+ * activations GELU(LN2(x') W1^T + b1) [B,S,F].  Same arguments as tt_workspace_bytes.  Replaces the
+ * stage CAPTURE of the reference's fused kernels (kernels/csrc/sequence_resident.cu:30-39,
+ * kernels/fused_megakernel.py:224-238), compared against eager in
+ * benchmarks/benchmark_steps_1_2.py:73-117. */
+int tt_stage_offsets(int batch, int seq, int d_model, int num_heads, int ffn_dim, int num_layers,
+                     int plan, int64_t* qkv, int64_t* ctx, int64_t* hidden);
+
 /* Whole forward of the block stack + final norm:
  *   y = mask(final_norm(block_L(...block_1(x)))), block(x) = mask(x' + W2 gelu(W1 LN2(x') + b1)
  *   + b2) with x' = x + mask(Wo attn(LN1 x) + bo)

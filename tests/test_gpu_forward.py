@@ -270,3 +270,50 @@ def test_folded_layernorm_matches_fused_ln_plan(device, name):
     print(f"[fold] {name} layerwise {res_a} fused_ln {res_b}", flush=True)
     assert res_a["passed"] and res_b["passed"]
     assert (ya.float() - yb.float()).abs().max().item() <= 1e-2
+
+
+# ---------------------------------------------------------------- captured stages of the fused plans
+@pytest.mark.parametrize("plan_name,shape", [
+    ("megakernel", (2, 64, 256, 8, 1024, True, True)),      # hd 32, causal, padded
+    ("megakernel", (1, 64, 256, 4, 1024, False, False)),    # hd 64
+    ("fused_ln", (2, 100, 128, 4, 512, True, True)),
+    ("layerwise", (4, 128, 256, 4, 1024, False, True)),     # LayerNorm folded (narrow tiles)
+    ("layerwise", (2, 256, 512, 8, 2048, True, False)),     # MFMA tiles; LN2 overwrites ctx
+], ids=["mk-hd32-causal-mask", "mk-hd64", "fusedln-causal-mask", "lw-fold-mask", "lw-mfma-causal"])
+def test_captured_stages(device, plan_name, shape):
+    """Per-stage parity inside the fused plans (after benchmarks/benchmark_steps_1_2.py:73-117 and
+    the CAPTURE slots of kernels/fused_megakernel.py:224-238): the last layer's Q / K / V, attention
+    context and GELU activations left in the workspace by one 1-layer forward, against the
+    oracle's stages.  The in-LDS LayerNorms of the megakernel and the fused-LN tiles are never
+    stored on their own; Q / K / V and the GELU input depend on them directly."""
+    from tttj_2026_amd import PLAN_FUSED_LN, PLAN_MEGAKERNEL
+    plans = {"megakernel": PLAN_MEGAKERNEL, "fused_ln": PLAN_FUSED_LN, "layerwise": PLAN_LAYERWISE}
+    b, s, d, h, f, causal, masked = shape
+    cfg = TransformerConfig(b, s, d, h, f, 1, causal)
+    model = build_model(cfg, seed=41)
+    with torch.no_grad():  # non-default LayerNorm affine parameters
+        g = torch.Generator().manual_seed(42)
+        for name, p in model.named_parameters():
+            if "norm" in name:
+                p.add_(0.2 * torch.randn(p.shape, generator=g))
+    x16, mask = make_inputs(cfg, masked, 43)
+    gm = copy.deepcopy(model).half().to(device).eval()
+    mod = make_optimized_transformer(copy.deepcopy(gm), plan=plans[plan_name])
+    print(f"[stages] {plan_name} {shape}", flush=True)
+    with torch.inference_mode():
+        mod(x16.to(device), None if mask is None else mask.to(device))
+        got = mod.captured_stages(b, s)
+        got = {k: (None if v is None else v.float().cpu()) for k, v in got.items()}
+    st = {}
+    O.forward(O.params_fp32(gm), x16.float(), mask, h, causal, stages=st)
+    v = torch.ones(b, s, dtype=torch.bool) if mask is None else mask
+    heads_to_rows = lambda t: t.permute(0, 2, 1, 3).reshape(b, s, d)  # [B,H,S,hd] -> [B,S,D]
+    checks = {"q": (heads_to_rows(got["q"]), st["q"]), "k": (heads_to_rows(got["k"]), st["k"]),
+              "v": (heads_to_rows(got["v"]), st["v"]), "hidden": (got["hidden"], st["gelu"])}
+    if got["ctx"] is not None:
+        checks["ctx"] = (got["ctx"], st["ctx"])
+    elif plan_name != "layerwise" or d <= 256:
+        raise AssertionError("the fused plans keep the context")
+    for name, (a, want) in checks.items():
+        err = (a[v] - want[v]).abs().max().item()
+        assert err <= 2e-2, (name, err)

@@ -231,3 +231,20 @@ def test_megakernel_workspaces_are_bounded(monkeypatch):
     mod._mega_entry(1, 68, 0, 16, cpu)                          # evicts (1, 65)
     assert list(mod._mega) == [(1, 66, 0), (1, 67, 0), (1, 64, 0), (1, 68, 0)]
     assert len(mod._mega) == OT.MEGA_WORKSPACES_KEPT
+
+
+def test_stage_offsets():
+    """tt_stage_offsets: the layer-wise workspace order (x', context / LN output, Q|K|V^T, hidden)
+    and which plans keep the attention context."""
+    T, D, F, B, S = 8192, 1024, 4096, 2, 4096
+    q, c, h = _lib.stage_offsets(B, S, D, 16, F, 12, _lib.PLAN_LAYERWISE)
+    assert q == 2 * T * D * 2 and c == -1 and h == q + (2 * T * D + B * D * S) * 2
+    q, c, h = _lib.stage_offsets(4, 128, 256, 4, 1024, 2, _lib.PLAN_LAYERWISE)  # folded LN
+    assert c == 512 * 256 * 2 and q == 2 * c
+    q, c, h = _lib.stage_offsets(2, 100, 128, 4, 512, 2, _lib.PLAN_FUSED_LN)
+    assert c >= 0
+    n = _lib.workspace_bytes(1, 64, 256, 8, 1024, 2, _lib.PLAN_MEGAKERNEL)
+    q, c, h = _lib.stage_offsets(1, 64, 256, 8, 1024, 2, _lib.PLAN_MEGAKERNEL)
+    assert len({q, c, h}) == 3 and max(q, c, h) < n
+    with pytest.raises(ValueError):
+        _lib.stage_offsets(1, 64, 240, 5, 1024, 1, _lib.PLAN_LAYERWISE)

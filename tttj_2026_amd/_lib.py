@@ -31,6 +31,8 @@ SIGNATURES = {
                               ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
     "tt_workspace_bytes": (_I, [_I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_I64)]),
     "tt_resolve_plan": (_I, [_I, _I, _I, _I, _I, _I]),
+    "tt_stage_offsets": (_I, [_I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_I64),
+                              ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
     "tt_megakernel_status": (_I, [_P, _I, _I, _I, _I, _I, ctypes.POINTER(_I), _P]),
     "tt_megakernel_tasks": (_I, [_I, _I, _I, _I, _I, _I]),
     "tt_megakernel_error_offset": (_I, [_I, _I, _I, _I, _I, _I, ctypes.POINTER(_I64)]),
@@ -109,6 +111,17 @@ def workspace_bytes(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int
     check(load().tt_workspace_bytes(batch, seq, d_model, heads, ffn_dim, num_layers, plan,
                                     ctypes.byref(out)), "tt_workspace_bytes")
     return out.value
+
+
+def stage_offsets(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int, num_layers: int,
+                  plan: int):
+    """(qkv, ctx, hidden) byte offsets of the last layer's intermediates in a forward's workspace
+    (``tt_stage_offsets``; ctx is -1 where the plan overwrites it)."""
+    q, c, h = _I64(), _I64(), _I64()
+    check(load().tt_stage_offsets(batch, seq, d_model, heads, ffn_dim, num_layers, plan,
+                                  ctypes.byref(q), ctypes.byref(c), ctypes.byref(h)),
+          "tt_stage_offsets")
+    return q.value, c.value, h.value
 
 
 def megakernel_error_offset(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,

@@ -61,6 +61,7 @@ struct Workspace {
   half *xa, *xn, *qkv, *hbuf;
   float2* part;   // partial row statistics of the residual stream, D / 4 slots per row at most
   int32_t* info;
+  size_t off_xn, off_qkv, off_hbuf;  // byte offsets of xn, qkv and hbuf from the base
   size_t bytes;
 };
 
@@ -74,13 +75,23 @@ static Workspace carve(char* base, int64_t B, int64_t S, int64_t D, int64_t F) {
     return p;
   };
   w.xa = (half*)take(T * D * 2);
+  w.off_xn = o;
   w.xn = (half*)take(T * D * 2);  // LN1 output of layer 0, then the attention context
+  w.off_qkv = o;
   w.qkv = (half*)take((2 * T * D + B * D * Sp) * 2);
+  w.off_hbuf = o;
   w.hbuf = (half*)take(T * F * 2);
   w.part = (float2*)take(T * (D / 4) * sizeof(float2));
   w.info = (int32_t*)take(2 * B * 4);
   w.bytes = o;
   return w;
+}
+
+// Whether the layer-wise plan folds LN2 (and LN1 of layers >= 1) into the next projection: only
+// where both QKV and ffn_in run on the narrow / small kernels (few tokens).
+static bool folds_layernorm(bool fused_ln, int64_t T, int64_t D, int64_t F) {
+  return !fused_ln && linear_is_narrow((int)T, (int)(3 * D), (int)D, TT_EPI_QKV) &&
+         linear_is_narrow((int)T, (int)F, (int)D, TT_EPI_BIAS_GELU);
 }
 
 static int check_model_shape(int B, int S, int D, int H, int F, int L) {
@@ -173,6 +184,31 @@ extern "C" int tt_workspace_bytes(int batch, int seq, int d_model, int num_heads
   } else {
     *bytes = (int64_t)carve(nullptr, batch, seq, d_model, ffn_dim).bytes;
   }
+  return TT_OK;
+}
+
+extern "C" int tt_stage_offsets(int batch, int seq, int d_model, int num_heads, int ffn_dim,
+                                int num_layers, int plan, int64_t* qkv, int64_t* ctx,
+                                int64_t* hidden) {
+  int rc = check_model_shape(batch, seq, d_model, num_heads, ffn_dim, num_layers);
+  if (rc != TT_OK) return rc;
+  TT_REQUIRE(qkv && ctx && hidden, "stage_offsets: null output");
+  TT_REQUIRE(plan >= TT_PLAN_AUTO && plan <= TT_PLAN_FUSED_LN, "stage_offsets: bad plan %d", plan);
+  plan = resolve_plan(plan, batch, seq, d_model, num_heads, ffn_dim);
+  if (plan == TT_PLAN_MEGAKERNEL) {
+    if ((rc = megakernel_supported(batch, seq, d_model, num_heads, ffn_dim, num_layers)) != TT_OK)
+      return rc;
+    megakernel_stage_offsets(batch, seq, d_model, ffn_dim, num_layers, qkv, ctx, hidden);
+    return TT_OK;
+  }
+  const Workspace w = carve(nullptr, batch, seq, d_model, ffn_dim);
+  *qkv = (int64_t)w.off_qkv;
+  *hidden = (int64_t)w.off_hbuf;
+  // the context buffer is overwritten by the LN2 output unless LN2 is fused or folded
+  const bool fused_ln = plan == TT_PLAN_FUSED_LN;
+  *ctx = (fused_ln || folds_layernorm(fused_ln, (int64_t)batch * seq, d_model, ffn_dim))
+             ? (int64_t)w.off_xn
+             : -1;
   return TT_OK;
 }
 
@@ -276,8 +312,7 @@ int transformer_fwd(const void* weights, const void* x, const uint8_t* mask, voi
   // the narrow / small kernels (the statistics loads overlap their K loop).  On the MFMA tiles of
   // larger shapes the epilogue work it adds is exposed and costs more than the LayerNorm launch
   // it removes (measured on MI355X: C5 +3.9%, C4 +5.5%), so LN1 / LN2 stay standalone there.
-  const bool fold = !fused_ln && linear_is_narrow(T, 3 * D, D, TT_EPI_QKV) &&
-                    linear_is_narrow(T, F, D, TT_EPI_BIAS_GELU);
+  const bool fold = folds_layernorm(fused_ln, T, D, F);
   const half* cur = (const half*)x;
   for (int l = 0; l < L; ++l) {
     const half* w = wts + (size_t)l * lay.stride;

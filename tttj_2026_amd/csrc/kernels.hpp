@@ -64,6 +64,11 @@ int launch_attention_wide(const AttnArgs& args, const int32_t* info, int head_di
 int launch_attention_small(const AttnArgs& args, const int32_t* info, int head_dim, int causal,
                            hipStream_t stream);
 
+// Byte offsets, in the megakernel's workspace, of the last layer's Q / K / V^T planes (the
+// TT_EPI_QKV layout), attention context [T, D] and FFN hidden activations [T, F].
+void megakernel_stage_offsets(int B, int S, int D, int F, int L, int64_t* qkv, int64_t* ctx,
+                              int64_t* hidden);
+
 // Persistent whole-model megakernel (megakernel.hip).  The workspace must be zero-filled before
 // its first use and then reused unchanged between launches of the same shape.
 size_t megakernel_workspace_bytes(int B, int S, int D, int F, int L);

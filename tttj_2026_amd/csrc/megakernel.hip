@@ -972,6 +972,14 @@ size_t megakernel_workspace_bytes(int B, int S, int D, int F, int L) {
   return mega_layout(B, S, D, F, L).bytes;
 }
 
+void megakernel_stage_offsets(int B, int S, int D, int F, int L, int64_t* qkv, int64_t* ctx,
+                              int64_t* hidden) {
+  const MegaLayout m = mega_layout(B, S, D, F, L);
+  *qkv = (int64_t)m.qkv;
+  *ctx = (int64_t)m.ctx;
+  *hidden = (int64_t)m.hbuf;
+}
+
 int megakernel_supported(int B, int S, int D, int H, int F, int L) {
   TT_REQUIRE(D / H == 32 || D / H == 64, "megakernel: head_dim %d not in {32, 64}", D / H);
   TT_REQUIRE(D % 64 == 0 && F % 64 == 0, "megakernel: d_model and ffn_dim must be multiples of 64");

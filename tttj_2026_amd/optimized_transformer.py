@@ -314,6 +314,37 @@ class OptimizedTransformer(nn.Module):
         return y
 
 
+    def captured_stages(self, batch: int, seq: int) -> Dict[str, Optional[torch.Tensor]]:
+        """Intermediates of the LAST layer of the most recent forward of shape (batch, seq), read
+        back from its workspace (the fused plans never materialise them otherwise; the reference
+        captures them from inside its fused kernels for its stage checks):
+        ``q``, ``k``, ``v`` [B, H, S, hd] (q divided back by the softmax factor the projection
+        applies), ``ctx`` [B, S, D] (None where the plan overwrites it) and ``hidden`` [B, S, F]
+        (GELU output).  Valid until the next forward on this module."""
+        cfg = self.config
+        plan = _lib.resolve_plan(batch, seq, cfg.d_model, cfg.num_heads, cfg.ffn_dim, self.plan)
+        ws = self.last_workspace
+        if ws is None:
+            raise RuntimeError("no forward has run on this module")
+        oq, oc, oh = _lib.stage_offsets(batch, seq, cfg.d_model, cfg.num_heads, cfg.ffn_dim,
+                                        cfg.num_layers, plan)
+        d, h, f = cfg.d_model, cfg.num_heads, cfg.ffn_dim
+        hd, t, sp = d // h, batch * seq, (seq + 63) // 64 * 64
+
+        def view(off: int, n: int) -> torch.Tensor:
+            return ws[off:off + 2 * n].view(torch.float16)
+
+        plane = t * d
+        qkv = view(oq, 2 * plane + batch * d * sp)
+        scale = hd ** -0.5 * 1.4426950408889634
+        q = (qkv[:plane].view(batch, h, seq, hd).float() / scale).half()
+        k = qkv[plane:2 * plane].view(batch, h, seq, hd)
+        v = qkv[2 * plane:].view(batch, h, hd, sp)[..., :seq].transpose(-1, -2)
+        ctx = None if oc < 0 else view(oc, t * d).view(batch, seq, d)
+        hidden = view(oh, t * f).view(batch, seq, f)
+        return {"q": q, "k": k, "v": v, "ctx": ctx, "hidden": hidden}
+
+
 class GraphedOptimizedTransformer(nn.Module):
     """HIP-graph replay around an ``OptimizedTransformer`` (the reference's
     ``GraphedHybridTransformer``, kernels/layerwise_hybrid.py:364-446).
