@@ -396,7 +396,7 @@ def test_gelu_epilogue_matches_exact_erf_gelu(device):
     """GELU epilogue on every fp16 pre-activation in [-12, 12]: the GEMM is arranged so that the
     accumulator equals the value exactly (x = [v, 0, ...], every weight row = e_0, bias 0), and the
     fp16 output must equal the correctly rounded exact-erf GELU (float64 math.erf) up to one fp16
-    ulp, with at most 0.1% of values off by that ulp (values within ~1e-7 of a rounding tie)."""
+    ulp, with at most 0.1% of values off by that ulp (values next to a rounding tie)."""
     vals = torch.arange(-(2 ** 15), 2 ** 15, dtype=torch.int32).to(torch.int16).view(torch.float16)
     vals = vals[torch.isfinite(vals) & (vals.float().abs() <= 12)]
     m, n, k = vals.numel(), 64, 64
