@@ -171,9 +171,10 @@ int tt_linear_fwd(const void* x, const void* w, const void* bias, const void* re
                   const uint8_t* valid, void* y, int m, int n, int k, int epilogue, int batch,
                   int seq, int heads, void* stream);
 
-/* Test hook: force tile configuration `index` (0: 256x256, 1: 256x128, 2: 128x128, 3: 128x64,
- * 4: 64x64, 5: 32x32 narrow tiles with K split over the block's waves) for every later GEMM whose N
- * it divides; -1 restores the automatic choice.  Process
+/* Test hook: force tile configuration `index` (0: 256x256 on 8 waves, 1: 256x128, 2: 128x128,
+ * 3: 128x64, 4: 64x64, 5: 32x32 narrow tiles with K split over the block's waves; 6-9: 128x256,
+ * 128x128, 128x64, 256x128 staged through registers; 10: 256x128 on 8 waves with a three-stage
+ * K ring) for every later GEMM whose N it divides; -1 restores the automatic choice.  Process
  * wide, not thread-safe.  No counterpart in the reference (its tile choices are compile-time
  * constants per case, kernels/fused_megakernel.py:121-171). */
 int tt_gemm_tile_override(int index);

@@ -144,9 +144,16 @@ __device__ void fill_padded_tile(const EpiArgs& ep, int M, int m0, int n0) {
 // a (BM / (NW / 2)) x (BN / 2) block of C as FM x FN 32x32 MFMA tiles.  Two 4-wave blocks of up to
 // 128 x 128 share a CU (one's epilogue runs beside the other's main loop); an 8-wave block puts two
 // waves on every SIMD by itself.
+// K stages in the LDS ring: three for the 8-wave 256 x 128 direct-copy tile (3 x 48 KiB), so a
+// stage's copies are issued two stages before it is read; two for every other tile.
+constexpr int gemm_stages(int bm, int bn, int path, int nw) {
+  return (path == 0 && nw == 8 && bm * bn <= 256 * 128) ? 3 : 2;
+}
+
 template <int BM, int BN, int MODE, int PATH, int NW = 4>
 __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1) void gemm_kernel(
     const half* __restrict__ X, const half* __restrict__ W, int M, int N, int K, EpiArgs ep) {
+  constexpr int NS = gemm_stages(BM, BN, PATH, NW);
   constexpr int WGM = NW / 2;
   constexpr int WM = BM / WGM, WN = BN / 2;
   constexpr int FM = WM / 32, FN = WN / 32;
@@ -281,25 +288,64 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1)
       }
     };
 
-    // Prologue: stage 0.  Then two stages per iteration, so both buffers are constant offsets
-    // (fragment reads use immediate offsets).  Before each stage: its copies have landed in LDS
-    // (vmcnt 0: every copy of this wave is older than the ones the stage issues) and every wave
-    // is done reading the buffer the stage's own copies overwrite.
+    if constexpr (NS == 2) {
+      // Prologue: stage 0.  Then two stages per iteration, so both buffers are constant offsets
+      // (fragment reads use immediate offsets).  Before each stage: its copies have landed in LDS
+      // (vmcnt 0: every copy of this wave is older than the ones the stage issues) and every wave
+      // is done reading the buffer the stage's own copies overwrite.
 #pragma unroll
-    for (int i = 0; i < NL; ++i) copy(i, 0, lds);
-    int kt = 0;
-    for (; kt + 2 <= nk; kt += 2) {
-      wait_vmcnt<0>();
-      raw_barrier();
-      stage(lds, lds + STAGE, kt + 1);
-      wait_vmcnt<0>();
-      raw_barrier();
-      stage(lds + STAGE, lds, kt + 2);
-    }
-    if (kt < nk) {
-      wait_vmcnt<0>();
-      raw_barrier();
-      stage(lds, lds + STAGE, kt + 1);
+      for (int i = 0; i < NL; ++i) copy(i, 0, lds);
+      int kt = 0;
+      for (; kt + 2 <= nk; kt += 2) {
+        wait_vmcnt<0>();
+        raw_barrier();
+        stage(lds, lds + STAGE, kt + 1);
+        wait_vmcnt<0>();
+        raw_barrier();
+        stage(lds + STAGE, lds, kt + 2);
+      }
+      if (kt < nk) {
+        wait_vmcnt<0>();
+        raw_barrier();
+        stage(lds, lds + STAGE, kt + 1);
+      }
+    } else {
+      // Three-buffer ring, three stages per iteration (constant buffers again).  Stage kt reads
+      // buffer kt % 3 and issues the copies of stage kt + 2 into buffer (kt + 2) % 3, the one stage
+      // kt - 1 read.  Before stage kt each wave waits until at most NL of its copies are in flight
+      // (those of stage kt + 1; copies complete in issue order), and the barrier makes every
+      // wave's copies of stage kt visible and frees the buffer of stage kt - 1.  Copies past the
+      // last stage re-read it into a buffer no remaining stage reads: (kt + 2) % 3 differs from
+      // (nk - 1) % 3 for kt = nk - 2 and nk - 1.
+      half* const s0 = lds;
+      half* const s1 = lds + STAGE;
+      half* const s2 = lds + 2 * STAGE;
+#pragma unroll
+      for (int i = 0; i < NL; ++i) copy(i, 0, s0);
+#pragma unroll
+      for (int i = 0; i < NL; ++i) copy(i, 1, s1);
+      int kt = 0;
+      for (; kt + 3 <= nk; kt += 3) {
+        wait_vmcnt<NL>();
+        raw_barrier();
+        stage(s0, s2, kt + 2);
+        wait_vmcnt<NL>();
+        raw_barrier();
+        stage(s1, s0, kt + 3);
+        wait_vmcnt<NL>();
+        raw_barrier();
+        stage(s2, s1, kt + 4);
+      }
+      if (kt < nk) {
+        wait_vmcnt<NL>();
+        raw_barrier();
+        stage(s0, s2, kt + 2);
+      }
+      if (kt + 1 < nk) {
+        wait_vmcnt<NL>();
+        raw_barrier();
+        stage(s1, s0, kt + 3);
+      }
     }
     wait_vmcnt<0>();  // the re-read copies past the end land before the epilogue reuses LDS
 
@@ -803,8 +849,9 @@ struct TileCfg {
 template <int BM, int BN, int MODE, int PATH, int NW = 4>
 static int run_tile(const half* x, const half* w, int m, int n, int k, const EpiArgs& ep,
                     hipStream_t stream) {
-  // double-buffered K stages; the epilogue stages the whole BM x BN tile in the same memory
-  const size_t lds = std::max(2 * (size_t)(BM + BN) * (PATH ? kBK + 8 : kBK), (size_t)BM * BN) *
+  // the K-stage ring; the epilogue stages the whole BM x BN tile in the same memory
+  constexpr size_t NS = gemm_stages(BM, BN, PATH, NW);
+  const size_t lds = std::max(NS * (BM + BN) * (PATH ? kBK + 8 : kBK), (size_t)BM * BN) *
                      sizeof(half);
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
@@ -832,15 +879,17 @@ static int run_mode(int tile, const half* x, const half* w, int m, int n, int k,
     case 7: return run_tile<128, 128, MODE, 1>(x, w, m, n, k, ep, stream);
     case 8: return run_tile<128, 64, MODE, 1>(x, w, m, n, k, ep, stream);
     case 9: return run_tile<256, 128, MODE, 1>(x, w, m, n, k, ep, stream);
+    case 10: return run_tile<256, 128, MODE, 0, 8>(x, w, m, n, k, ep, stream);
     default: return run_tile<64, 64, MODE, 0>(x, w, m, n, k, ep, stream);
   }
 }
 
 // index 0: 256 x 256 on 8 waves; index 5: 32 x 32 narrow tiles (gemm_narrow_kernel), chosen for
 // grids that leave most CUs idle; indices 6-9: 128 x 256, 128 x 128, 128 x 64, 256 x 128 on the
-// register path
+// register path; index 10: 256 x 128 on 8 waves with a three-stage ring
 static const TileCfg kTiles[] = {{256, 256}, {256, 128}, {128, 128}, {128, 64}, {64, 64},
-                                 {32, 32},   {128, 256}, {128, 128}, {128, 64}, {256, 128}};
+                                 {32, 32},   {128, 256}, {128, 128}, {128, 64}, {256, 128},
+                                 {256, 128}};
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
 static int g_tile_override = -1;  // test hook: force one tile configuration
@@ -852,13 +901,17 @@ static int g_tile_override = -1;  // test hook: force one tile configuration
 // GELU, 71 against 76 us with bias only); with 1.5 rounds (QKV, N = 3072) or half a round (N =
 // 1024) two 128 x 128 blocks per CU are faster (QKV 57 against 63 us, ffn_out 65 against 95 us).
 // Narrower tiles are used when a wider one would leave CUs idle, down to the 32x32 narrow kernel
-// for few-token grids.
-static int pick_tile(int m, int n, int k, int mode, int cus) {
+// for few-token grids.  Exactly one round of 8-wave 256 x 128 tiles with the three-stage ring
+// (N = 1024 at M = 8192) beats two 128 x 128 blocks per CU when no row mask is given (out_proj
+// 25.6 -> 24.3 us, ffn_out 72.6 -> 69.2 us); with a row mask, 128-row tiles skip more padded
+// rows and stay faster (the same shapes at 20% padding: 25.0 against 26.2, 68.2 against 71.0 us).
+static int pick_tile(int m, int n, int k, int mode, int cus, bool masked = false) {
   (void)mode;
   if (g_tile_override >= 0 && g_tile_override < kNumTiles && n % kTiles[g_tile_override].bn == 0)
     return g_tile_override;
   auto tiles = [&](int i) { return (long)((m + kTiles[i].bm - 1) / kTiles[i].bm) * (n / kTiles[i].bn); };
   if (n % 256 == 0 && tiles(0) >= 2 * cus && tiles(0) % cus == 0) return 0;
+  if (!masked && n % 128 == 0 && k >= 1024 && tiles(10) == cus) return 10;
   // One round of 128 x 64 tiles streaming a long K is latency-bound: each CU moves only the bytes
   // it keeps in flight, and the register path keeps two more K stages in flight than the direct
   // copies (measured on MI355X, 4096 x 512 x 2048: 22.3 -> 15.8 us).  On grids of several tiles
@@ -936,7 +989,7 @@ int launch_linear(const half* x, const half* w, int m, int n, int k, const EpiAr
   }
   if (m == 0) return TT_OK;
   if (k % kBK != 0 || n % 64 != 0) return run_small(ep.mode, x, w, m, n, k, ep, stream);
-  const int tile = pick_tile(m, n, k, ep.mode, device_cus());
+  const int tile = pick_tile(m, n, k, ep.mode, device_cus(), ep.valid != nullptr);
   if (tile == 5) return run_narrow(ep.mode, x, w, m, n, k, ep, stream);
   switch (ep.mode) {
     case TT_EPI_BIAS: return run_mode<TT_EPI_BIAS>(tile, x, w, m, n, k, ep, stream);
