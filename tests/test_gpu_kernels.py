@@ -318,6 +318,32 @@ def test_attention(device, hd, causal, s, mask_kind):
         assert err <= 6e-3, err
 
 
+@pytest.mark.parametrize("hd", [32, 64])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("s", [2048, 2100])
+@pytest.mark.parametrize("mask_kind", ["none", "prefix", "nonprefix", "ragged_empty"])
+def test_attention_long_ring(device, hd, causal, s, mask_kind):
+    """Sequences of 2048 keys and more run the three-tile key ring (head_dim <= 64); 2100 ends in
+    a partial tile."""
+    b, h = 2, 2
+    q = _rand((b, h, s, hd), 70 + s, 1.5)
+    k = _rand((b, h, s, hd), 71 + s, 1.5)
+    sp = (s + 63) // 64 * 64
+    vt = _rand((b, h, hd, sp), 72 + s, 1.0)
+    vt[..., s:] = float("nan")
+    mask = _masks(mask_kind, b, s, 73 + s)
+    ctx = ops.attention(q, k, vt, None if mask is None else mask.to(device), causal)
+    torch.cuda.synchronize()
+    ref = _attention_ref(q, k, vt, mask, causal)
+    got = ctx.float().cpu()
+    assert torch.isfinite(got).all()
+    if mask is not None:
+        assert _bits_zero(ctx.cpu()[~mask])
+        got, ref = got[mask], ref[mask]
+    if got.numel():
+        assert (got - ref).abs().max().item() <= 6e-3
+
+
 @pytest.mark.parametrize("b,s,h,hd,causal", [(2, 4096, 16, 64, True), (8, 1024, 16, 64, True),
                                               (8, 512, 8, 64, False), (1, 64, 8, 32, True)])
 def test_attention_benchmark_shapes(device, b, s, h, hd, causal):

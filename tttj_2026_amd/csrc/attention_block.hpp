@@ -2,9 +2,10 @@
 // attention kernel and the persistent megakernel).
 //
 // One 256-thread block owns (sequence b, head h, 128-query tile); each of its four waves owns 32
-// queries.  Key/value tiles of 64 keys are staged in LDS (double-buffered) by buffer -> LDS
-// dwordx4 copies issued one tile ahead, so no registers hold in-flight tiles; each lane's source
-// offset is fixed and the tile start moves the wave-uniform buffer base.
+// queries.  Key/value tiles of 64 keys are staged in LDS (double-buffered, or a ring of three for
+// long sequences) by buffer -> LDS dwordx4 copies issued one (two) tiles ahead, so no registers
+// hold in-flight tiles; each lane's source offset is fixed and the tile start moves the
+// wave-uniform buffer base.
 // Per wave and tile:
 //   S^T = K Q^T   with v_mfma_f32_32x32x16_f16 (K from LDS as the A operand, Q^T held in
 //                 registers as the B operand), so lane l holds one query (l % 32) and 32 of the 64
@@ -85,10 +86,13 @@ struct AttnArgs {
 
 // One (sequence b, head h, 128-query tile qt) attention block on 256 threads.  kv_end is
 // 1 + the index of the last valid key of sequence b (S without a mask) and `prefix` says whether
-// the valid keys form a prefix; sk_base / sv_base are 2 * 64 * HD halfs of LDS each.  POLICY is
-// the cache policy of the Q, K and V^T loads (kLoadDevice when other workgroups of the same
-// launch wrote them).
-template <int HD, bool CAUSAL, int POLICY = kLoadDefault>
+// the valid keys form a prefix; sk_base / sv_base are 2 * 64 * HD halfs of LDS each, or 3 * 64 *
+// HD with RING3 (three key tiles in flight, so a tile's copies are issued two tiles before it is
+// read; a compile-time choice: with a run-time buffer index the compiler can no longer tell the
+// in-flight copies from the tile being read and waits for all of them before its first MFMA).
+// POLICY is the cache policy of the Q, K and V^T loads (kLoadDevice when other workgroups of the
+// same launch wrote them).
+template <int HD, bool CAUSAL, int POLICY = kLoadDefault, bool RING3 = false>
 __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int qt, int kv_end,
                                                 bool prefix, half* sk_base, half* sv_base) {
   static_assert(HD == 32 || HD == 64 || HD == 128 || HD == 256, "MFMA attention head_dim");
@@ -116,6 +120,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
   const int ldv = round_up(S, kBKV);
 
   const bool keymask = (mask != nullptr) && !prefix;
+  constexpr bool r3 = RING3;
 
   const int q0 = qt * kBQ;
   const int qw = q0 + wave * 32;
@@ -205,10 +210,11 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
 #pragma unroll
   for (int e = 0; e < 16; ++e) sinit[e] = 0.f;
 
-  // Non-prefix masks: this lane's key-mask byte for the current and the next tile, loaded when
-  // the tile's copies are issued so the end-of-tile wait covers it.
-  // The raw byte is kept (address clamped, bound applied at use) so the load's wait lands at the
-  // use, not at the load.
+  // Non-prefix masks: this lane's key-mask byte.  Ring of two: the next tile's byte is loaded
+  // when its copies are issued, so the end-of-tile wait covers it.  Ring of three: each tile's
+  // byte is loaded at the start of that tile (a byte carried over two tiles would make its
+  // register moves wait for every load issued before it).  The raw byte is kept (address
+  // clamped, bound applied at use) so the load's wait lands at the use, not at the load.
   auto mask_byte = [&](int t0) -> int {
     const int key = min(t0 + lane, S - 1);
     return mask[(size_t)b * S + key];
@@ -216,7 +222,10 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
   int mcur = 0, mnext = 0;
   if (ntiles > 0) {
     issue_tile(0, 0);
-    if (keymask) mcur = mask_byte(0);
+    if (!r3 && keymask) mcur = mask_byte(0);
+    // Both first tiles land before the loop: with copies still in flight on entry, the compiler
+    // adds a wait for the next tile's copies before every tile's first MFMA.
+    if (r3 && ntiles > 1) issue_tile(kBKV, 1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (kBKV > S) {
@@ -225,11 +234,16 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     }
   }
   for (int t = 0; t < ntiles; ++t) {
-    const int st = t & 1;
+    const int st = r3 ? t % 3 : (t & 1);
     const int t0 = t * kBKV;
-    if (t + 1 < ntiles) {
+    if (!r3 && t + 1 < ntiles) {
       issue_tile(t0 + kBKV, st ^ 1);
       if (keymask) mnext = mask_byte(t0 + kBKV);
+    }
+    // Ring of three: the copies of tile t + 2 go to the buffer tile t - 1 used.
+    if (r3) {
+      if (keymask) mcur = mask_byte(t0);
+      if (t + 2 < ntiles) issue_tile(t0 + 2 * kBKV, st == 0 ? 2 : st - 1);
     }
     if (wave_active && t0 < wave_end) {
       floatx16 s[2];
@@ -319,12 +333,21 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
           }
       }
     }
-    mcur = mnext;
+    if (!r3) mcur = mnext;
     if (t + 1 < ntiles) {
-      __builtin_amdgcn_s_waitcnt(0);  // the next tile's copies have landed ...
-      __syncthreads();                // ... and every wave is done with this one
+      const int sn = r3 ? (st == 2 ? 0 : st + 1) : (st ^ 1);
+      if (r3 && t + 2 < ntiles) {
+        // The next tile's copies have landed (those of tile t + 2, issued after them, may stay
+        // in flight) ...
+        wait_vmcnt<KCOPIES + VCOPIES>();
+        raw_barrier();                  // ... and every wave is done with this one (the LDS
+                                        // reads fed this tile's MFMAs, so they have returned)
+      } else {
+        __builtin_amdgcn_s_waitcnt(0);  // the next tile's copies have landed ...
+        __syncthreads();                // ... and every wave is done with this one
+      }
       if (t0 + 2 * kBKV > S) {        // next tile is the partial last one
-        clear_vt_tail(t0 + kBKV, st ^ 1);
+        clear_vt_tail(t0 + kBKV, sn);
         __syncthreads();
       }
     }
@@ -347,16 +370,23 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     }
 }
 
+// Key tiles in flight in the standalone kernel: three for long sequences up to head_dim 64
+// (48 KiB per block at 64, still three blocks per CU), two otherwise (a third 32 / 64 KiB tile
+// would cost a block per CU above head_dim 64).  Measured on MI355X: the ring of three is 2-4%
+// faster at B 2, S 4096 (causal) but 1-3% slower at S 512 / 1024, where blocks run few tiles.
+constexpr bool attention_ring3_hd(int hd) { return hd <= 64; }
+inline bool attention_ring3(int hd, int seq) { return attention_ring3_hd(hd) && seq >= 2048; }
+
 // Standalone launch: one block per (b, h, 128-query tile).  `info` (or nullptr without a mask)
 // holds kv_end per sequence and whether its valid keys form a prefix (mask_info_kernel).
-template <int HD, bool CAUSAL>
+template <int HD, bool CAUSAL, bool RING3>
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a, const int32_t* __restrict__ info) {
   // Dynamic LDS: with statically declared tiles the compiler makes the first K-fragment read of
   // every tile wait (vmcnt(0)) for the next tile's in-flight global -> LDS copies, serialising
   // the prefetch; from the dynamic area it relies on the explicit waits, as intended.
   extern __shared__ __align__(16) half att_lds[];
   half* sk = att_lds;
-  half* sv = att_lds + 2 * kBKV * HD;
+  half* sv = att_lds + (RING3 ? 3 : 2) * kBKV * HD;
   const int BH = a.B * a.H;
   const int nqt = (a.S + kBQ - 1) / kBQ;
   const int bh = blockIdx.x % BH;
@@ -369,29 +399,40 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a, const int32_
     kv_end = info[b];
     prefix = info[a.B + b] != 0;
   }
-  attention_block<HD, CAUSAL>(a, bh, qt, kv_end, prefix, sk, sv);
+  attention_block<HD, CAUSAL, kLoadDefault, RING3>(a, bh, qt, kv_end, prefix, sk, sv);
 }
 
-constexpr size_t attention_lds_bytes(int hd) { return 4 * (size_t)kBKV * hd * sizeof(half); }
+constexpr size_t attention_lds_bytes(int hd, bool ring3 = false) {
+  return 2 * (size_t)(ring3 ? 3 : 2) * kBKV * hd * sizeof(half);
+}
 
-// Host side: one launch of attention_kernel<HD, CAUSAL> over every (b, h, query tile); the
-// dynamic LDS limit is raised once per instantiation (above 64 KiB for HD 256).
-template <int HD, bool CAUSAL>
-int launch_attention_hd(const AttnArgs& args, const int32_t* info, hipStream_t stream) {
+// Host side: one launch of attention_kernel<HD, CAUSAL, RING3> over every (b, h, query tile);
+// the dynamic LDS limit is raised once per instantiation (above 64 KiB for HD 256).
+template <int HD, bool CAUSAL, bool RING3>
+int launch_attention_ring(const AttnArgs& args, const int32_t* info, hipStream_t stream) {
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
-    attr = hipFuncSetAttribute((const void*)attention_kernel<HD, CAUSAL>,
+    attr = hipFuncSetAttribute((const void*)attention_kernel<HD, CAUSAL, RING3>,
                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)attention_lds_bytes(HD));
+                               (int)attention_lds_bytes(HD, RING3));
   });
   if (attr != hipSuccess)
     return fail(TT_ERR_HIP, "hipFuncSetAttribute(attention hd %d): %s", HD, hipGetErrorString(attr));
   const long blocks = (long)args.B * args.H * ((args.S + kBQ - 1) / kBQ);
   TT_REQUIRE(blocks < (1L << 31), "attention: grid too large");
-  hipLaunchKernelGGL((attention_kernel<HD, CAUSAL>), dim3((unsigned)blocks), dim3(256),
-                     attention_lds_bytes(HD), stream, args, info);
+  hipLaunchKernelGGL((attention_kernel<HD, CAUSAL, RING3>), dim3((unsigned)blocks), dim3(256),
+                     attention_lds_bytes(HD, RING3), stream, args, info);
   return launch_status("attention_kernel");
+}
+
+// The key-tile ring chosen for the sequence length.
+template <int HD, bool CAUSAL>
+int launch_attention_hd(const AttnArgs& args, const int32_t* info, hipStream_t stream) {
+  if constexpr (attention_ring3_hd(HD)) {
+    if (attention_ring3(HD, args.S)) return launch_attention_ring<HD, CAUSAL, true>(args, info, stream);
+  }
+  return launch_attention_ring<HD, CAUSAL, false>(args, info, stream);
 }
 
 }  // namespace tt
