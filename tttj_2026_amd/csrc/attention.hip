@@ -1,8 +1,8 @@
 // Flash-attention launches for head_dim 32, 64 and 128 (attention_kernel, one block per (b, h,
 // 128-query tile); the block itself is attention_block() in attention_block.hpp), the head_dim
 // dispatch (8 / 16: attention_small.hip, 256: attention_wide.hip) and the per-sequence mask
-// summary.  Built with the VGPR-form MFMA flag (accumulators in architectural VGPRs: 127 VGPRs at
-// head_dim 64, 190 at 128).
+// summary.  Built with the VGPR-form MFMA flag (accumulators in architectural VGPRs: 138-140 VGPRs
+// at head_dim 64, three waves per SIMD; 199-203 at 128, two).
 #include "attention_block.hpp"
 #include "kernels.hpp"
 
