@@ -331,7 +331,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the forward shards by sequence with zero collectives; see DESIGN.md)",
+              "(the forward would shard by sequence with zero collectives; not built)",
               file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
