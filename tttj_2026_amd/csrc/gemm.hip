@@ -201,10 +201,12 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  // The block's bias slice goes to LDS once (made visible by the prologue's barrier).
-  __shared__ __align__(16) half sbias[BN];
-  if (threadIdx.x < BN / 8)
-    *(u32x4*)(sbias + 8 * threadIdx.x) = *(const u32x4*)(ep.bias + n0 + 8 * threadIdx.x);
+  // The block's bias slice goes to LDS once, as fp32 (made visible by the prologue's barrier).
+  __shared__ __align__(16) float sbias[BN];
+  if (threadIdx.x < BN / 4) {
+    const half4 b = *(const half4*)(ep.bias + n0 + 4 * threadIdx.x);
+    *(floatx4*)(sbias + 4 * threadIdx.x) = floatx4{(float)b[0], (float)b[1], (float)b[2], (float)b[3]};
+  }
   constexpr bool ZERO_MASKED = MODE == TT_EPI_BIAS || MODE == TT_EPI_BIAS_GELU || MODE == TT_EPI_QKV;
 
   // Fragment addressing: A = W rows (output features), B = X rows (tokens); lane l reads row
@@ -461,24 +463,30 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1)
   // when they store).
   float qs = 1.f;  // Q columns of the QKV projection carry ep.q_scale
   if constexpr (MODE == TT_EPI_QKV) qs = n0 < ep.d_model ? ep.q_scale : 1.f;
+  bool keep[FM];
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
-    const int ml = j * 32 + (lane & 31);
-    bool keep = true;
-    if constexpr (ZERO_MASKED) keep = ep.valid == nullptr || ep.valid[min(mw + ml, M - 1)] != 0;
+    keep[j] = true;
+    if constexpr (ZERO_MASKED)
+      keep[j] = ep.valid == nullptr || ep.valid[min(mw + j * 32 + (lane & 31), M - 1)] != 0;
+  }
+  // Columns outermost: each lane reads its 4 bias values of a column group once for all FM rows.
 #pragma unroll
-    for (int i = 0; i < FN; ++i) {
+  for (int i = 0; i < FN; ++i) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int nl = i * 32 + 8 * g + 4 * (lane >> 5);
-        const half4 bv = *(const half4*)(sbias + wn * WN + nl);
+    for (int g = 0; g < 4; ++g) {
+      const int nl = i * 32 + 8 * g + 4 * (lane >> 5);
+      const floatx4 bv = *(const floatx4*)(sbias + wn * WN + nl);
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const int ml = j * 32 + (lane & 31);
         half4 h;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float v = acc[i][j][4 * g + e] + (float)bv[e];
+          float v = acc[i][j][4 * g + e] + bv[e];
           if constexpr (MODE == TT_EPI_BIAS_GELU) v = gelu_erf(v);
           if constexpr (MODE == TT_EPI_QKV) v *= qs;
-          h[e] = keep ? (half)v : (half)0.f;
+          h[e] = keep[j] ? (half)v : (half)0.f;
         }
         if (vt_scalar) {
           if (mw + ml < M) store_vt4(ep, mw + ml, nw + nl, h);
