@@ -34,7 +34,7 @@ import time
 
 import torch
 
-from tttj_2026_amd import _lib, make_optimized_transformer, ops, roofline
+from tttj_2026_amd import PLAN_LAYERWISE, _lib, make_optimized_transformer, ops, roofline
 from tttj_2026_amd.configs import (REFERENCE_CASES, SEED, WORKLOADS, WORKLOAD_ORDER, build_model,
                                    make_inputs, reference_case_config, workload_inputs)
 
@@ -134,40 +134,67 @@ def bench_model(cfg, x16, mask, steps, warmup, rounds, eager, dev, xd=None):
 
 
 def kernel_breakdown(name, dev, iters=20):
-    """Time each kernel of one layer in isolation (HIP events on the launch stream)."""
+    """Time each kernel of one layer in isolation (HIP events on the launch stream), on the data
+    the forward itself runs them on: one forward of the workload leaves its last layer's Q / K /
+    V^T (Q pre-multiplied by the softmax factor, the form its attention launches read), LN2 output
+    and GELU activations in the workspace, and the GEMMs use that layer's packed weights.  The
+    attention is the forward's variant (tt_attention_fwd_prescaled).  For masked workloads the
+    forward packs the valid tokens; these isolated GEMMs run all B*S rows (an upper bound)."""
     cfg = WORKLOADS[name].config
-    B, S, D, H, F = cfg.batch_size, cfg.seq_len, cfg.d_model, cfg.num_heads, cfg.ffn_dim
-    T, hd = B * S, D // H
+    B, S, D, H, F, L = (cfg.batch_size, cfg.seq_len, cfg.d_model, cfg.num_heads, cfg.ffn_dim,
+                        cfg.num_layers)
+    T, hd, Sp = B * S, D // H, (S + 63) // 64 * 64
     x16, mask = workload_inputs(name)
-    g = torch.Generator().manual_seed(5)
-    rnd = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).half().to(dev)
-    x = x16.to(dev).reshape(T, D)
+    model = build_model(cfg).half().to(dev).eval()
+    opt = make_optimized_transformer(copy.deepcopy(model), plan=PLAN_LAYERWISE)
+    xd = x16.to(dev)
     md = None if mask is None else mask.to(dev)
-    lnw, lnb = rnd(D, sc=0.1) + 1, rnd(D, sc=0.1)
-    wqkv, bqkv = rnd(3 * D, D, sc=D ** -0.5), rnd(3 * D, sc=0.1)
-    wo, bo = rnd(D, D, sc=D ** -0.5), rnd(D, sc=0.1)
-    w1, b1 = rnd(F, D, sc=D ** -0.5), rnd(F, sc=0.1)
-    w2, b2 = rnd(D, F, sc=F ** -0.5), rnd(D, sc=0.1)
-    xn = ops.layernorm(x, lnw, lnb)
-    q, k, vt = ops.qkv_projection(xn.reshape(B, S, D), wqkv, bqkv, H)
-    ctx = ops.attention(q, k, vt, md, cfg.causal).reshape(T, D)
-    hmid = ops.linear(xn, w1, b1, "gelu")
-    resid = x.clone()
+    with torch.inference_mode():
+        opt(xd, md)
+    torch.cuda.synchronize()
+    ws = opt.last_workspace
+    oq, _, oh = _lib.stage_offsets(B, S, D, H, F, L, PLAN_LAYERWISE)
+    half = lambda off, n: ws[off:off + 2 * n].view(torch.float16)
+    plane = T * D
+    qkv = half(oq, 2 * plane + B * D * Sp)
+    q, k, vt = (qkv[:plane].view(B, H, S, hd), qkv[plane:2 * plane].view(B, H, S, hd),
+                qkv[2 * plane:].view(B, H, hd, Sp))
+    xa = half(0, plane).view(T, D).clone()                     # residual stream
+    xn = half((T * D * 2 + 255) // 256 * 256, plane).view(T, D).clone()   # LN2 output
+    hmid = half(oh, T * F).view(T, F).clone()                  # GELU activations
+    offs, stride, final_off, _ = _lib.weight_layout(D, F, L)
+    wl = opt.packed_weights[(L - 1) * stride:]
+    seg = lambda i, n: wl[offs[i]:offs[i] + n]
+    lnw, lnb = seg(6, D), seg(7, D)
+    wqkv, bqkv = seg(2, 3 * D * D).view(3 * D, D), seg(3, 3 * D)
+    wo, bo = seg(4, D * D).view(D, D), seg(5, D)
+    w1, b1 = seg(8, F * D).view(F, D), seg(9, F)
+    w2, b2 = seg(10, D * F).view(D, F), seg(11, D)
+    ctx = ops.attention(q, k, vt, md, cfg.causal, prescaled=True).reshape(T, D)
+    resid = xa.clone()
     lens = lengths_of(mask, cfg)
     lf = roofline.layer_flops(cfg, lens)
-    # The LayerNorm launch (a few microseconds) is timed through the C ABI with a preallocated
-    # output: the Python wrapper's per-call overhead is longer than the kernel and would leave the
-    # GPU idle between back-to-back launches.
+    # The short launches (LayerNorm, attention) are timed through the C ABI with preallocated
+    # outputs (and the mask summary computed once): the Python wrappers' per-call overhead would
+    # otherwise leave the GPU idle between back-to-back launches.
     lib = _lib.load()
-    y_ln = torch.empty_like(x)
-    ln_args = (x.data_ptr(), lnw.data_ptr(), lnb.data_ptr(), None, y_ln.data_ptr(), T, D, 1e-5,
-               torch.cuda.current_stream(dev).cuda_stream)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    y_ln = torch.empty_like(xa)
+    ln_args = (xa.data_ptr(), lnw.data_ptr(), lnb.data_ptr(), None, y_ln.data_ptr(), T, D, 1e-5,
+               stream)
     _lib.check(lib.tt_layernorm_fwd(*ln_args), "tt_layernorm_fwd")
+    info = None if md is None else ops.mask_info(md, B, S, dev)
+    ctx_out = torch.empty(B, S, D, dtype=torch.float16, device=dev)
+    att_args = (q.data_ptr(), k.data_ptr(), vt.data_ptr(), None if md is None else md.data_ptr(),
+                None if info is None else info.data_ptr(), ctx_out.data_ptr(), B, S, H, hd,
+                int(cfg.causal), stream)
+    _lib.check(lib.tt_attention_fwd_prescaled(*att_args), "tt_attention_fwd_prescaled")
     kernels = {
         "layernorm": (lambda: lib.tt_layernorm_fwd(*ln_args), 2, "hbm", roofline.layernorm_bytes(T, D)),
         "gemm_qkv": (lambda: ops.qkv_projection(xn.reshape(B, S, D), wqkv, bqkv, H), 1, "mfma",
                      2 * T * 3 * D * D),
-        "attention": (lambda: ops.attention(q, k, vt, md, cfg.causal), 1, "mfma", lf["attention"]),
+        "attention": (lambda: lib.tt_attention_fwd_prescaled(*att_args), 1, "mfma",
+                      lf["attention"]),
         "gemm_out": (lambda: ops.linear(ctx, wo, bo, "resid_masked", residual=resid, valid=md,
                                         out=resid), 1, "mfma", 2 * T * D * D),
         "gemm_ffn_in": (lambda: ops.linear(xn, w1, b1, "gelu"), 1, "mfma", 2 * T * D * F),

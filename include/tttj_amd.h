@@ -86,17 +86,24 @@ int tt_weight_layout(int d_model, int ffn_dim, int num_layers,
 int tt_pack_derived(void* weights, int d_model, int ffn_dim, int num_layers, void* stream);
 
 /* Execution plans of tt_transformer_fwd. */
-#define TT_PLAN_AUTO 0       /* fused-LN layer-wise plan for d_model <= 128 and at most 2048
-                              * tokens, else layer-wise */
+#define TT_PLAN_AUTO 0       /* the persistent megakernel for at most 64 tokens with d_model
+                              * 256..512 (multiples of 64), ffn_dim a multiple of 64 and head_dim
+                              * 32 or 64; else the fused-LN layer-wise plan for d_model <= 128
+                              * (multiple of 64, ffn_dim too) and at most 2048 tokens; else
+                              * layer-wise.  When AUTO resolves to the megakernel
+                              * (tt_resolve_plan), its workspace rules apply: zero-filled before
+                              * the first call and kept for that one shape. */
 #define TT_PLAN_LAYERWISE 1  /* one launch per op: LN, GEMMs with fused epilogues, attention */
 #define TT_PLAN_MEGAKERNEL 2 /* one persistent launch (<= one workgroup per CU) for the stack */
 #define TT_PLAN_FUSED_LN 3   /* layer-wise with LN1 / LN2 computed inside the QKV / ffn_in GEMM
                               * tiles (five launches per layer; d_model <= 512) */
 
 /* Bytes of workspace tt_transformer_fwd needs for this shape and plan.  The workspace of the
- * megakernel plan holds its dependency counters and launch epoch: it must be zero-filled before
- * its first use and then passed unchanged to every later call with the same shape (it is not
- * re-entrant: calls that share it must be ordered on one stream).  Replaces the workspace
+ * megakernel plan -- asked for, or picked by TT_PLAN_AUTO for few tokens (tt_resolve_plan says
+ * which) -- holds its dependency counters and launch epoch: it must be zero-filled before its
+ * first use and then passed unchanged to every later call with the same shape (one workspace per
+ * shape; it is not re-entrant: calls that share it must be ordered on one stream).  Layer-wise
+ * workspaces need no initial contents and may be shared by calls of any shape that fits.  Replaces the workspace
  * allocation of fused_megakernel_forward / dag_megakernel_forward
  * (kernels/fused_megakernel.py:1928-1937, kernels/dag_megakernel.py:2092-2097) and the persistent
  * scheduler buffer of SequenceResidentTransformer (kernels/sequence_resident.py:148-150). */
@@ -174,7 +181,8 @@ int tt_linear_fwd(const void* x, const void* w, const void* bias, const void* re
 /* Test hook: force tile configuration `index` (0: 256x256 on 8 waves, 1: 256x128, 2: 128x128,
  * 3: 128x64, 4: 64x64, 5: 32x32 narrow tiles with K split over the block's waves; 6-9: 128x256,
  * 128x128, 128x64, 256x128 staged through registers; 10: 256x128 on 8 waves with a three-stage
- * K ring) for every later GEMM whose N it divides; -1 restores the automatic choice.  Process
+ * K ring; 11, 12: 256x256 / 256x128 on 8 waves with 32-deep K stages in a 4- / 6-stage ring) for
+ * every later GEMM whose N it divides; -1 restores the automatic choice.  Process
  * wide, not thread-safe.  No counterpart in the reference (its tile choices are compile-time
  * constants per case, kernels/fused_megakernel.py:121-171). */
 int tt_gemm_tile_override(int index);
@@ -197,12 +205,36 @@ int tt_attention_fwd(const void* q, const void* k, const void* vt, const uint8_t
                      const int32_t* info, void* ctx, int batch, int seq, int heads, int head_dim,
                      int causal, void* stream);
 
+/* 1 if tt_transformer_fwd with a mask runs this shape on packed variable-length rows, 0 if it
+ * runs every token (padded rows skipped per tile), < 0 on bad arguments.  Packed rows: the valid
+ * tokens of every sequence, in order, become the rows of the residual stream, the LayerNorm
+ * output, the attention context and the FFN hidden activations (a right-padded sequence of l
+ * valid tokens takes min(l rounded up to 8, S) rows, any other mask its valid count), and the
+ * LayerNorms and GEMMs run over those rows only; the row count stays on the device.  Taken by
+ * the layer-wise plan when all four projections run on MFMA tiles.  No counterpart in the
+ * reference, which masks padded rows but computes them (kernels/fused_megakernel.py:628-638);
+ * its prefix-length extraction is kernels/case14_hybrid.py:645-669. */
+int tt_forward_packs_rows(int batch, int seq, int d_model, int num_heads, int ffn_dim, int plan);
+
+/* Test hook: 0 makes every later masked forward run all tokens (no packed rows), -1 restores the
+ * automatic choice.  Process wide, not thread-safe.  No counterpart in the reference. */
+int tt_forward_packing_override(int enable);
+
+/* tt_attention_fwd with q already multiplied by hd^-1/2 log2(e) and rounded to fp16 once -- the
+ * form the forward's QKV projection writes (tt_stage_offsets) and its attention launches read:
+ * ctx = softmax_2(q k^T) v with the same masks.  Replaces the same reference functions as
+ * tt_attention_fwd, for callers that fold the softmax scale into their Q projection. */
+int tt_attention_fwd_prescaled(const void* q, const void* k, const void* vt, const uint8_t* mask,
+                               const int32_t* info, void* ctx, int batch, int seq, int heads,
+                               int head_dim, int causal, void* stream);
+
 /* Where a forward's intermediates of its LAST layer are left in the workspace, for per-stage checks
  * of the fused plans (the megakernel's tasks and the fused-LN tiles never materialise LN1 / LN2 or
  * the other stages on their own): byte offsets of the Q / K / V^T planes (the TT_EPI_QKV layout;
  * Q is stored multiplied by hd^-1/2 log2(e), the form the attention kernels read), of the attention
  * context [B,S,D] (-1 when the plan overwrites it with the LN2 output) and of the FFN hidden
- * activations GELU(LN2(x') W1^T + b1) [B,S,F].  Same arguments as tt_workspace_bytes.  Replaces the
+ * activations GELU(LN2(x') W1^T + b1) [B,S,F] (in packed-row order, see tt_forward_packs_rows,
+ * after a masked forward that packs rows).  Same arguments as tt_workspace_bytes.  Replaces the
  * stage CAPTURE of the reference's fused kernels (kernels/csrc/sequence_resident.cu:30-39,
  * kernels/fused_megakernel.py:224-238), compared against eager in
  * benchmarks/benchmark_steps_1_2.py:73-117. */
@@ -239,10 +271,19 @@ int tt_noalloc_scratch_bytes(int64_t* bytes);
  * launch.  Same arguments, plans and results as tt_transformer_fwd.  Every call on one GPU shares
  * that GPU's array: calls that overlap on one GPU (other streams, threads) race on it, so order
  * them on one stream.  The megakernel plan clears its dependency counters at the start of each
- * call (a fill kernel, no memset). */
+ * call (a fill kernel, no memset), which also clears the previous call's error word: read it with
+ * tt_noalloc_status before the next call. */
 int tt_transformer_fwd_noalloc(const void* weights, const void* x, const uint8_t* mask, void* y,
                                int batch, int seq, int d_model, int num_heads, int ffn_dim,
                                int num_layers, int causal, int plan, void* stream);
+
+/* Health of the latest tt_transformer_fwd_noalloc call on the current device (synchronises
+ * `stream`): *status = 0 when it ran a layer-wise plan or every dependency wait of its megakernel
+ * launch completed, 1 if a wait gave up (that call wrote NaN over all of y).  Read it after the
+ * call and before the next one, whose counter reset clears the word.  No counterpart in the
+ * reference (its waits are unbounded, kernels/dag_megakernel.py:1355-1367); the no-alloc entry
+ * point itself exists for callers that cannot allocate (graph capture, serving loops). */
+int tt_noalloc_status(int* status, void* stream);
 
 #ifdef __cplusplus
 }

@@ -55,7 +55,7 @@ GEMM_SHAPES = [(64, 768, 256), (100, 64, 64), (512, 1024, 256), (4096, 1536, 512
                (130, 256, 192)]
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12])
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
 def test_linear_bias_all_tiles(device, m, n, k, tile):
     if tile >= 0 and m * n * k > 2 ** 31:
@@ -121,7 +121,7 @@ def _padded_rows(m, seed):
     return v
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 2, 4, 5, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [-1, 0, 2, 4, 5, 6, 7, 8, 9, 10, 11, 12])
 @pytest.mark.parametrize("mode", ["bias", "gelu", "resid_masked", "masked_resid"])
 @pytest.mark.parametrize("m,n,k,seq", [(1000, 512, 256, 0), (4096, 1024, 512, 0),
                                        (4096, 1024, 512, 512), (8192, 256, 256, 1024)])
@@ -163,7 +163,7 @@ def test_linear_masked_rows(device, m, n, k, seq, mode, tile):
         assert _bits_zero(got[~v])
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 2, 4, 5, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [-1, 0, 2, 4, 5, 6, 7, 8, 9, 10, 11, 12])
 @pytest.mark.parametrize("b,s,d,h", [(4, 256, 512, 8), (3, 100, 256, 4), (2, 1024, 1024, 16),
                                      (4, 100, 32, 4), (2, 130, 96, 3), (3, 128, 128, 16),
                                      (2, 64, 1024, 4), (2, 72, 128, 1), (5, 3, 64, 2),
@@ -316,6 +316,34 @@ def test_attention(device, hd, causal, s, mask_kind):
     if got.numel():
         err = (got - ref).abs().max().item()
         assert err <= 6e-3, err
+
+
+@pytest.mark.parametrize("hd", [8, 32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("s", [200, 2100])
+@pytest.mark.parametrize("mask_kind", ["none", "prefix", "nonprefix"])
+def test_attention_prescaled_entry(device, hd, causal, s, mask_kind):
+    """tt_attention_fwd_prescaled (Q already multiplied by hd^-1/2 log2 e and rounded once, the
+    form the forward's QKV epilogue writes) against tt_attention_fwd, which applies the factor
+    when it loads Q: the MFMA kernels round Q * factor to fp16 the same way, so the two agree
+    bit for bit; the head_dim 8 / 16 kernel keeps Q * factor in fp32, so there they agree to
+    rounding."""
+    b, h = 2, 2
+    q = _rand((b, h, s, hd), 90 + s, 1.5)
+    k = _rand((b, h, s, hd), 91 + s, 1.5)
+    vt = _rand((b, h, hd, (s + 63) // 64 * 64), 92 + s, 1.0)
+    mask = _masks(mask_kind, b, s, 93 + s)
+    mdev = None if mask is None else mask.to(device)
+    f32 = lambda v: torch.tensor(v, dtype=torch.float32)
+    factor = (f32(1.0) / torch.sqrt(f32(float(hd)))) * f32(1.4426950408889634)
+    qs = (q.float() * factor.to(device)).half()
+    a = ops.attention(q, k, vt, mdev, causal)
+    c = ops.attention(qs, k, vt, mdev, causal, prescaled=True)
+    torch.cuda.synchronize()
+    if hd >= 32:
+        assert torch.equal(a, c)
+    else:
+        assert (a.float() - c.float()).abs().max().item() <= 4e-3
 
 
 @pytest.mark.parametrize("hd", [32, 64])

@@ -104,6 +104,27 @@ def test_plan_resolution():
         _lib.resolve_plan(1, 64, 256, 8, 1024, 7)
 
 
+def _documented_auto_plan(b, s, d, h, f):
+    """TT_PLAN_AUTO as include/tttj_amd.h documents it."""
+    hd = d // h
+    tiles64 = d % 64 == 0 and f % 64 == 0
+    if b * s <= 64 and 256 <= d <= 512 and tiles64 and hd in (32, 64):
+        return _lib.PLAN_MEGAKERNEL
+    if tiles64 and d <= 128 and b * s <= 2048:
+        return _lib.PLAN_FUSED_LN
+    return _lib.PLAN_LAYERWISE
+
+
+def test_auto_plan_matches_its_documentation():
+    for b in (1, 2, 4, 16, 64):
+        for s in (16, 32, 64, 100, 128):
+            for d, h, f in ((128, 4, 128), (128, 2, 512), (256, 8, 1024), (256, 4, 1024),
+                            (256, 16, 1024), (512, 8, 2048), (512, 16, 1536), (1024, 16, 4096),
+                            (96, 3, 128), (256, 4, 1000), (576, 9, 2304)):
+                got = _lib.resolve_plan(b, s, d, h, f, _lib.PLAN_AUTO)
+                assert got == _documented_auto_plan(b, s, d, h, f), (b, s, d, h, f, got)
+
+
 @pytest.mark.parametrize("kwargs,ok", [
     (dict(d_model=256, num_heads=8, ffn_dim=1024), True),     # hd 32
     (dict(d_model=1024, num_heads=16, ffn_dim=4096), True),   # hd 64
@@ -222,15 +243,41 @@ def test_megakernel_workspaces_are_bounded(monkeypatch):
     cfg = TransformerConfig(1, 64, 256, 8, 1024, 4, True)
     mod = OT.OptimizedTransformer(build_model(cfg), plan=OT.PLAN_MEGAKERNEL)
     monkeypatch.setattr(mod, "_attach", lambda entry, b, s: None)
+    detached = []
+    monkeypatch.setattr(mod, "_detach", lambda entry, b, s: detached.append((b, s, entry[0])))
     monkeypatch.setattr(mod, "_new_status_word", lambda: torch.zeros(1, dtype=torch.int32))
     cpu = torch.device("cpu")
     first = mod._mega_entry(1, 64, 0, 16, cpu)[0]
     for s in (65, 66, 67):
         mod._mega_entry(1, s, 0, 16, cpu)
+    evicted = mod._mega[(1, 65, 0)][0]
     assert mod._mega_entry(1, 64, 0, 16, cpu)[0] is first     # reused, now most recent
     mod._mega_entry(1, 68, 0, 16, cpu)                          # evicts (1, 65)
     assert list(mod._mega) == [(1, 66, 0), (1, 67, 0), (1, 64, 0), (1, 68, 0)]
     assert len(mod._mega) == OT.MEGA_WORKSPACES_KEPT
+    # the evicted workspace's status word was detached before the entry was dropped
+    assert len(detached) == 1 and detached[0][:2] == (1, 65) and detached[0][2] is evicted
+
+
+def test_pinned_megakernel_workspace_is_never_evicted(monkeypatch):
+    """A workspace a captured graph replays on (pinned) outlives any number of other shapes."""
+    from tttj_2026_amd import optimized_transformer as OT
+
+    cfg = TransformerConfig(1, 64, 256, 8, 1024, 4, True)
+    mod = OT.OptimizedTransformer(build_model(cfg), plan=OT.PLAN_MEGAKERNEL)
+    monkeypatch.setattr(mod, "_attach", lambda entry, b, s: None)
+    detached = []
+    monkeypatch.setattr(mod, "_detach", lambda entry, b, s: detached.append((b, s)))
+    monkeypatch.setattr(mod, "_new_status_word", lambda: torch.zeros(1, dtype=torch.int32))
+    cpu = torch.device("cpu")
+    kept = mod._mega_entry(1, 64, 0, 16, cpu)
+    assert mod.pin_workspace(1, 64, 0) is kept
+    for s in range(65, 75):
+        mod._mega_entry(1, s, 0, 16, cpu)
+    assert (1, 64, 0) in mod._mega and mod._mega[(1, 64, 0)] is kept
+    assert (1, 64) not in detached
+    assert len(mod._mega) == OT.MEGA_WORKSPACES_KEPT
+    assert mod.pin_workspace(1, 99, 0) is None   # no workspace of that shape (another plan)
 
 
 def test_stage_offsets():
@@ -248,3 +295,36 @@ def test_stage_offsets():
     assert len({q, c, h}) == 3 and max(q, c, h) < n
     with pytest.raises(ValueError):
         _lib.stage_offsets(1, 64, 240, 5, 1024, 1, _lib.PLAN_LAYERWISE)
+
+
+def test_forward_packs_rows_rule():
+    """Masked layer-wise forwards whose four projections run on MFMA tiles pack the valid tokens;
+    the few-token (narrow-tile, folded-LayerNorm), fused-LN and megakernel plans do not."""
+    assert _lib.forward_packs_rows(8, 512, 512, 8, 2048)          # C3
+    assert _lib.forward_packs_rows(8, 1024, 1024, 16, 4096)       # C4
+    assert _lib.forward_packs_rows(2, 4096, 1024, 16, 4096)       # C5 (only with a mask)
+    assert not _lib.forward_packs_rows(4, 128, 256, 4, 1024)      # C1: narrow tiles, LN folded
+    assert not _lib.forward_packs_rows(1, 64, 256, 8, 1024)       # C2: megakernel
+    assert not _lib.forward_packs_rows(2, 100, 128, 4, 512)       # fused-LN plan
+    assert not _lib.forward_packs_rows(8, 512, 512, 8, 2048, _lib.PLAN_MEGAKERNEL)
+    assert _lib.forward_packs_rows(8, 512, 512, 8, 2048, _lib.PLAN_LAYERWISE)
+    with pytest.raises(ValueError):
+        _lib.forward_packs_rows(8, 512, 512, 8, 2048, 9)
+
+
+def test_packed_row_tokens_layout():
+    """Host restatement of the packed layout: right-padded sequences take min(l rounded up to 8,
+    S) rows (the rows past l pad to 8, token -1), other masks their valid tokens in order."""
+    S = 12
+    mask = torch.zeros(4, S, dtype=torch.bool)
+    mask[0, :5] = True                 # prefix of 5 -> 8 rows
+    mask[2, :12] = True                # full -> 12 rows
+    mask[3, [1, 4, 5]] = True          # not a prefix -> its 3 valid tokens
+    rows = _lib.packed_row_tokens(mask, S)
+    assert rows[:8] == [0, 1, 2, 3, 4, -1, -1, -1]
+    assert rows[8:20] == list(range(24, 36))     # sequence 1 is empty
+    assert rows[20:] == [37, 40, 41]
+    assert len(rows) == 23
+    mask2 = torch.zeros(1, 10, dtype=torch.bool)
+    mask2[0, :9] = True                # 9 rounds up to 16, capped at S = 10
+    assert _lib.packed_row_tokens(mask2, 10) == list(range(9)) + [-1]

@@ -82,3 +82,40 @@ def test_noalloc_rejects_shapes_beyond_scratch(device):
                                         torch.cuda.current_stream(device).cuda_stream)
     assert rc == _lib.TT_ERR_INVALID
     assert "scratch" in _lib.last_error()
+
+
+def test_noalloc_status_reports_a_wait_that_gave_up(device):
+    """tt_noalloc_status: 0 after a good megakernel call, 1 after one whose dependency waits were
+    made to give up (test hook: spin limit 0, every wave still exits; y is all NaN), 0 again after
+    the next good call (whose counter reset clears the word)."""
+    lib = _lib_noalloc()
+    cfg = TransformerConfig(1, 64, 256, 8, 1024, 2, True)
+    gm = build_model(cfg, seed=25).half().to(device).eval()
+    opt = make_optimized_transformer(copy.deepcopy(gm))
+    x16, _ = make_inputs(cfg, False, 26)
+    xd = x16.to(device)
+    y = torch.empty_like(xd)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    status = ctypes.c_int(-1)
+
+    def call():
+        rc = lib.tt_transformer_fwd_noalloc(
+            opt.packed_weights.data_ptr(), xd.data_ptr(), None, y.data_ptr(), 1, 64,
+            cfg.d_model, cfg.num_heads, cfg.ffn_dim, cfg.num_layers, 1, PLAN_MEGAKERNEL, stream)
+        _lib.check(rc, "tt_transformer_fwd_noalloc")
+        _lib.check(lib.tt_noalloc_status(ctypes.byref(status), stream), "tt_noalloc_status")
+        return status.value
+
+    print("[noalloc] status: good call", flush=True)
+    assert call() == 0
+    assert torch.isfinite(y).all()
+    print("[noalloc] status: spin limit 0", flush=True)
+    assert lib.tt_megakernel_set_spin_limit(0) == 0
+    try:
+        bad = call()
+    finally:
+        lib.tt_megakernel_set_spin_limit(-1)
+    assert bad == 1
+    assert torch.isnan(y).all()
+    assert call() == 0
+    assert torch.isfinite(y).all()

@@ -31,6 +31,8 @@ SIGNATURES = {
                               ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
     "tt_workspace_bytes": (_I, [_I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_I64)]),
     "tt_resolve_plan": (_I, [_I, _I, _I, _I, _I, _I]),
+    "tt_forward_packs_rows": (_I, [_I, _I, _I, _I, _I, _I]),
+    "tt_forward_packing_override": (_I, [_I]),
     "tt_stage_offsets": (_I, [_I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_I64),
                               ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
     "tt_megakernel_status": (_I, [_P, _I, _I, _I, _I, _I, ctypes.POINTER(_I), _P]),
@@ -46,9 +48,11 @@ SIGNATURES = {
     "tt_pack_derived": (_I, [_P, _I, _I, _I, _P]),
     "tt_mask_info": (_I, [_P, _P, _I, _I, _P]),
     "tt_attention_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "tt_attention_fwd_prescaled": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "tt_transformer_fwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "tt_noalloc_scratch_bytes": (_I, [ctypes.POINTER(_I64)]),
     "tt_transformer_fwd_noalloc": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "tt_noalloc_status": (_I, [ctypes.POINTER(_I), _P]),
 }
 
 _lock = threading.Lock()
@@ -130,6 +134,31 @@ def megakernel_error_offset(batch: int, seq: int, d_model: int, heads: int, ffn_
     check(load().tt_megakernel_error_offset(batch, seq, d_model, heads, ffn_dim, num_layers,
                                             ctypes.byref(out)), "tt_megakernel_error_offset")
     return out.value
+
+
+def forward_packs_rows(batch: int, seq: int, d_model: int, num_heads: int, ffn_dim: int,
+                       plan: int = PLAN_AUTO) -> bool:
+    """Whether a masked forward of this shape runs on packed variable-length rows."""
+    rc = load().tt_forward_packs_rows(batch, seq, d_model, num_heads, ffn_dim, plan)
+    if rc < 0:
+        check(TT_ERR_INVALID, "tt_forward_packs_rows")
+    return bool(rc)
+
+
+def packed_row_tokens(mask, seq: int):
+    """Token index (b * S + s) of every packed row of a masked forward that packs rows, -1 for the
+    rows that pad a right-padded sequence to a multiple of 8 (the layout of
+    ``tt_forward_packs_rows``; computed on the host from a CPU bool mask [B, S])."""
+    rows = []
+    for b in range(mask.shape[0]):
+        valid = mask[b].nonzero().flatten().tolist()
+        kv_end = valid[-1] + 1 if valid else 0
+        if len(valid) == kv_end:  # right-padded prefix (or empty)
+            n = min((kv_end + 7) // 8 * 8, seq)
+            rows += [b * seq + s if s < kv_end else -1 for s in range(n)]
+        else:
+            rows += [b * seq + s for s in valid]
+    return rows
 
 
 def resolve_plan(batch: int, seq: int, d_model: int, num_heads: int, ffn_dim: int,

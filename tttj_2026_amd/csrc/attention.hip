@@ -9,7 +9,9 @@
 namespace tt {
 
 __global__ __launch_bounds__(256) void mask_info_kernel(const uint8_t* __restrict__ mask,
-                                                        int32_t* __restrict__ info, int B, int S) {
+                                                        int32_t* __restrict__ info,
+                                                        int32_t* __restrict__ counts, int B,
+                                                        int S) {
   const int b = blockIdx.x;
   int last = -1, count = 0;
   if (mask == nullptr) {
@@ -41,12 +43,15 @@ __global__ __launch_bounds__(256) void mask_info_kernel(const uint8_t* __restric
       info[b] = sl[0] + 1;
       info[B + b] = (sc[0] == sl[0] + 1) ? 1 : 0;
     }
+    if (counts != nullptr) counts[b] = sc[0];
   }
 }
 
-int launch_mask_info(const uint8_t* mask, int32_t* info, int batch, int seq, hipStream_t stream) {
+int launch_mask_info(const uint8_t* mask, int32_t* info, int batch, int seq, hipStream_t stream,
+                     int32_t* counts) {
   TT_REQUIRE(batch > 0 && seq > 0 && info != nullptr, "mask_info: bad arguments");
-  hipLaunchKernelGGL(mask_info_kernel, dim3(batch), dim3(256), 0, stream, mask, info, batch, seq);
+  hipLaunchKernelGGL(mask_info_kernel, dim3(batch), dim3(256), 0, stream, mask, info, counts,
+                     batch, seq);
   return launch_status("mask_info_kernel");
 }
 
@@ -63,13 +68,13 @@ float attention_q_scale(int head_dim) {
 
 int launch_attention(const half* q, const half* k, const half* vt, const uint8_t* mask,
                      const int32_t* info, half* ctx, int batch, int seq, int heads, int head_dim,
-                     int causal, hipStream_t stream, bool q_prescaled) {
+                     int causal, hipStream_t stream, bool q_prescaled, const int* out_row) {
   TT_REQUIRE(batch > 0 && seq > 0 && heads > 0, "attention: bad shape");
   int rc = attention_head_dim_supported(head_dim);
   if (rc != TT_OK) return rc;
   TT_REQUIRE(mask == nullptr || info != nullptr, "attention: a mask needs its mask_info");
   const AttnArgs args{q, k, vt, mask, ctx, batch, seq, heads, attention_q_scale(head_dim),
-                      q_prescaled ? 1 : 0};
+                      q_prescaled ? 1 : 0, out_row};
   if (head_dim <= 16) return launch_attention_small(args, info, head_dim, causal, stream);
   if (head_dim == 256) return launch_attention_wide(args, info, head_dim, causal, stream);
   switch (head_dim) {
@@ -95,4 +100,14 @@ extern "C" int tt_attention_fwd(const void* q, const void* k, const void* vt, co
   return tt::launch_attention((const tt::half*)q, (const tt::half*)k, (const tt::half*)vt, mask,
                               info, (tt::half*)ctx, batch, seq, heads, head_dim, causal,
                               (hipStream_t)stream);
+}
+
+extern "C" int tt_attention_fwd_prescaled(const void* q, const void* k, const void* vt,
+                                          const uint8_t* mask, const int32_t* info, void* ctx,
+                                          int batch, int seq, int heads, int head_dim, int causal,
+                                          void* stream) {
+  TT_REQUIRE(q && k && vt && ctx, "attention: null pointer");
+  return tt::launch_attention((const tt::half*)q, (const tt::half*)k, (const tt::half*)vt, mask,
+                              info, (tt::half*)ctx, batch, seq, heads, head_dim, causal,
+                              (hipStream_t)stream, true);
 }

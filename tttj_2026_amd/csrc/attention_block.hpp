@@ -82,6 +82,10 @@ struct AttnArgs {
   // Q already multiplied by scale_log2 (rounded to fp16 once, by the QKV projection's epilogue);
   // otherwise the block multiplies and rounds it when it loads it.
   int q_prescaled;
+  // Packed context rows (variable-length batches): out_row[b * S + s] is the row of token (b, s)
+  // in a context of only the valid tokens, -1 for a padded token (not stored).  nullptr: the
+  // context is token-major [B, S, D] and padded rows are written as +0.0.
+  const int* out_row = nullptr;
 };
 
 // One (sequence b, head h, 128-query tile qt) attention block on 256 threads.  kv_end is
@@ -354,10 +358,16 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
   }
 
   if (q >= S) return;
+  size_t orow = (size_t)b * S + q;
+  if (a.out_row != nullptr) {  // lanes l and l ^ 32 hold the same query: they leave together
+    const int r = a.out_row[orow];
+    if (r < 0) return;
+    orow = (size_t)r;
+  }
   const float l_tot = xhalf_sum(l_run);
   const bool qvalid = wave_active && q < kv_end && (mask == nullptr || mask[(size_t)b * S + q] != 0);
   const float inv = (qvalid && l_tot > 0.f) ? 1.0f / l_tot : 0.f;
-  half* dst = ctx + ((size_t)b * S + q) * D + (size_t)h * HD;
+  half* dst = ctx + orow * D + (size_t)h * HD;
 #pragma unroll
   for (int i = 0; i < DB; ++i)
 #pragma unroll
@@ -398,6 +408,24 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a, const int32_
   if (info != nullptr) {
     kv_end = info[b];
     prefix = info[a.B + b] != 0;
+  }
+  // A query tile at or past the last valid key holds only padded rows: they are +0.0 (or, with a
+  // packed output map, not stored at all), and the key loop -- whose copies and barriers such a
+  // block would otherwise run without any MFMA work, over the longest key range of the sequence --
+  // is skipped.
+  const int q0 = qt * kBQ;
+  if (q0 >= kv_end) {
+    if (a.out_row != nullptr) return;
+    constexpr int CPR = HD / 8;  // 16-byte chunks per context row
+    const size_t D = (size_t)a.H * HD;
+    const int h = bh - b * a.H;
+    for (int e = threadIdx.x; e < kBQ * CPR; e += 256) {
+      const int q = q0 + e / CPR;
+      if (q < a.S)
+        *(u32x4*)(a.ctx + ((size_t)b * a.S + q) * D + (size_t)h * HD + 8 * (e % CPR)) =
+            u32x4{0u, 0u, 0u, 0u};
+    }
+    return;
   }
   attention_block<HD, CAUSAL, kLoadDefault, RING3>(a, bh, qt, kv_end, prefix, sk, sv);
 }

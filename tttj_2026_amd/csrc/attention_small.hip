@@ -41,6 +41,14 @@ __global__ __launch_bounds__(kSmallBQ) void attention_small_kernel(AttnArgs a,
   const bool keymask = a.mask != nullptr && !prefix;
   const int tid = threadIdx.x;
   const int q0 = qt * kSmallBQ, q = q0 + tid;
+  if (q0 >= kv_end) {  // only padded queries: +0.0 rows (none with a packed context), no key loop
+    if (a.out_row == nullptr && q < S) {
+      half* dst = a.ctx + ((size_t)b * S + q) * ((size_t)H * HD) + (size_t)h * HD;
+#pragma unroll
+      for (int d0 = 0; d0 < HD; d0 += 8) *(u32x4*)(dst + d0) = u32x4{0u, 0u, 0u, 0u};
+    }
+    return;
+  }
   const int ldv = round_up(S, 64);
   const half* Qbh = a.Q + (size_t)bh * S * HD;
   const half* Kbh = a.K + (size_t)bh * S * HD;
@@ -100,9 +108,15 @@ __global__ __launch_bounds__(kSmallBQ) void attention_small_kernel(AttnArgs a,
   }
 
   if (q >= S) return;
+  size_t orow = (size_t)b * S + q;
+  if (a.out_row != nullptr) {  // packed context: padded tokens have no row
+    const int r = a.out_row[orow];
+    if (r < 0) return;
+    orow = (size_t)r;
+  }
   const bool qvalid = q < kv_end && (a.mask == nullptr || a.mask[(size_t)b * S + q] != 0);
   const float inv = (qvalid && l > 0.f) ? 1.0f / l : 0.f;
-  half* dst = a.ctx + ((size_t)b * S + q) * ((size_t)H * HD) + (size_t)h * HD;
+  half* dst = a.ctx + orow * ((size_t)H * HD) + (size_t)h * HD;
 #pragma unroll
   for (int d0 = 0; d0 < HD; d0 += 8) {
     half8 v;

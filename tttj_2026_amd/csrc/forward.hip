@@ -61,6 +61,11 @@ struct Workspace {
   half *xa, *xn, *qkv, *hbuf;
   float2* part;   // partial row statistics of the residual stream, D / 4 slots per row at most
   int32_t* info;
+  // packed variable-length rows (varlen.hip): valid counts per sequence, the packed row count,
+  // packed row -> token, token -> packed row, and packed row -> Q / K and V^T offsets
+  int32_t *vl_counts, *vl_n, *row_tok, *slot;
+  int2* rowmap;
+  uint8_t* pvalid;   // packed row -> valid token (0 for the rows that pad a sequence to 8)
   size_t off_xn, off_qkv, off_hbuf;  // byte offsets of xn, qkv and hbuf from the base
   size_t bytes;
 };
@@ -83,6 +88,12 @@ static Workspace carve(char* base, int64_t B, int64_t S, int64_t D, int64_t F) {
   w.hbuf = (half*)take(T * F * 2);
   w.part = (float2*)take(T * (D / 4) * sizeof(float2));
   w.info = (int32_t*)take(2 * B * 4);
+  w.vl_counts = (int32_t*)take(B * 4);
+  w.vl_n = (int32_t*)take(4);
+  w.row_tok = (int32_t*)take(T * 4);
+  w.slot = (int32_t*)take(T * 4);
+  w.rowmap = (int2*)take(T * sizeof(int2));
+  w.pvalid = (uint8_t*)take(T);
   w.bytes = o;
   return w;
 }
@@ -92,6 +103,22 @@ static Workspace carve(char* base, int64_t B, int64_t S, int64_t D, int64_t F) {
 static bool folds_layernorm(bool fused_ln, int64_t T, int64_t D, int64_t F) {
   return !fused_ln && linear_is_narrow((int)T, (int)(3 * D), (int)D, TT_EPI_QKV) &&
          linear_is_narrow((int)T, (int)F, (int)D, TT_EPI_BIAS_GELU);
+}
+
+// Whether a masked layer-wise forward packs the valid tokens (varlen.hip): when the LayerNorms
+// are not fused or folded and all four projections run on the MFMA tiles (the packed row count
+// is read on the device by those kernels), and the Q / V^T planes stay below 2^31 elements.
+static bool g_packing_off = false;  // test hook (tt_forward_packing_override)
+
+static bool packs_rows(bool fused_ln, bool fold, int64_t B, int64_t S, int64_t D, int64_t H,
+                       int64_t F) {
+  const int64_t T = B * S, Sp = (S + 63) / 64 * 64;
+  if (g_packing_off || fused_ln || fold || T * D >= (1LL << 31) || B * D * Sp >= (1LL << 31))
+    return false;
+  return !linear_is_narrow((int)T, (int)(3 * D), (int)D, TT_EPI_QKV) &&
+         !linear_is_narrow((int)T, (int)D, (int)D, TT_EPI_RESID_MASKED) &&
+         !linear_is_narrow((int)T, (int)F, (int)D, TT_EPI_BIAS_GELU) &&
+         !linear_is_narrow((int)T, (int)D, (int)F, TT_EPI_MASKED_RESID) && H > 0;
 }
 
 static int check_model_shape(int B, int S, int D, int H, int F, int L) {
@@ -110,7 +137,9 @@ static int check_model_shape(int B, int S, int D, int H, int F, int L) {
 
 using namespace tt;
 
-extern "C" const char* tt_version(void) { return "tttj_amd 0.1 gfx950"; }
+// 0.2: 18 segments per layer in the packed weights (tt_pack_derived fills 12-17; the folded
+// LayerNorm and megakernel paths read them), packed variable-length rows for masked batches.
+extern "C" const char* tt_version(void) { return "tttj_amd 0.2 gfx950"; }
 
 extern "C" const char* tt_last_error_string(void) { return g_last_error.c_str(); }
 
@@ -224,6 +253,29 @@ extern "C" int tt_resolve_plan(int batch, int seq, int d_model, int num_heads, i
   return resolve_plan(plan, batch, seq, d_model, num_heads, ffn_dim);
 }
 
+extern "C" int tt_forward_packing_override(int enable) {
+  TT_REQUIRE(enable == 0 || enable == -1, "forward_packing_override: %d is not 0 or -1", enable);
+  g_packing_off = enable == 0;
+  return TT_OK;
+}
+
+extern "C" int tt_forward_packs_rows(int batch, int seq, int d_model, int num_heads, int ffn_dim,
+                                     int plan) {
+  if (check_model_shape(batch, seq, d_model, num_heads, ffn_dim, 1) != TT_OK) return -1;
+  if (plan < TT_PLAN_AUTO || plan > TT_PLAN_FUSED_LN) {
+    fail(TT_ERR_INVALID, "forward_packs_rows: bad plan %d", plan);
+    return -1;
+  }
+  plan = resolve_plan(plan, batch, seq, d_model, num_heads, ffn_dim);
+  if (plan == TT_PLAN_MEGAKERNEL) return 0;
+  const bool fused_ln = plan == TT_PLAN_FUSED_LN;
+  const int64_t T = (int64_t)batch * seq;
+  return packs_rows(fused_ln, folds_layernorm(fused_ln, T, d_model, ffn_dim), batch, seq, d_model,
+                    num_heads, ffn_dim)
+             ? 1
+             : 0;
+}
+
 extern "C" int tt_megakernel_trace_fwd(const void* weights, const void* x, const uint8_t* mask,
                                        void* y, void* workspace, int64_t workspace_bytes,
                                        int batch, int seq, int d_model, int num_heads, int ffn_dim,
@@ -258,6 +310,80 @@ extern "C" int tt_megakernel_status(const void* workspace, int batch, int seq, i
 
 namespace tt {
 
+// Layer-wise forward over packed variable-length rows (varlen.hip has the layout): LayerNorms
+// and GEMMs run over the n packed rows only (n read on the device), the QKV epilogue scatters
+// packed rows into the token layout of Q / K / V^T, the attention stores each valid token's
+// context at its packed row, and the final LayerNorm scatters back to [B, S, D] with +0.0 for
+// padded tokens.  Seven launches per layer, as the padded plan.
+static int forward_packed(const half* wts, const Layout& lay, const half* x, const uint8_t* mask,
+                          half* y, const Workspace& ws, const int32_t* info, int B, int S, int D,
+                          int H, int F, int L, int causal, hipStream_t stream) {
+  const int T = B * S, hd = D / H;
+  const size_t plane = (size_t)T * D;
+  half* q = ws.qkv;
+  half* k = ws.qkv + plane;
+  half* vt = ws.qkv + 2 * plane;
+  int rc;
+  for (int l = 0; l < L; ++l) {
+    const half* w = wts + (size_t)l * lay.stride;
+    // LN1; in the first layer it also gathers the valid tokens of x into the packed residual
+    // stream (rows that pad a sequence to 8 get +0.0)
+    if (l == 0)
+      rc = launch_layernorm_rows(x, w + lay.off[0], w + lay.off[1], nullptr, ws.row_tok, ws.vl_n,
+                                 ws.xa, ws.xn, T, D, 1e-5f, stream);
+    else
+      rc = launch_layernorm_rows(ws.xa, w + lay.off[0], w + lay.off[1], nullptr, nullptr, ws.vl_n,
+                                 nullptr, ws.xn, T, D, 1e-5f, stream);
+    if (rc != TT_OK) return rc;
+    EpiArgs ep{};
+    ep.bias = w + lay.off[3];
+    ep.y = q;
+    ep.ldy = 3 * D;
+    ep.mode = TT_EPI_QKV;
+    ep.batch = B;
+    ep.seq = S;
+    ep.heads = H;
+    ep.head_dim = hd;
+    ep.d_model = D;
+    ep.q_scale = attention_q_scale(hd);
+    ep.m_dev = ws.vl_n;
+    ep.rowmap = ws.rowmap;
+    ep.valid = ws.pvalid;  // rows that pad a sequence to 8 write +0.0, as padded tokens do
+    if ((rc = launch_linear(ws.xn, w + lay.off[2], T, 3 * D, D, ep, stream)) != TT_OK) return rc;
+    if ((rc = launch_attention(q, k, vt, mask, info, ws.xn, B, S, H, hd, causal, stream, true,
+                               ws.slot)) != TT_OK)
+      return rc;
+    ep = EpiArgs{};
+    ep.bias = w + lay.off[5];
+    ep.resid = ws.xa;
+    ep.y = ws.xa;
+    ep.ldy = D;
+    ep.mode = TT_EPI_RESID_MASKED;
+    ep.m_dev = ws.vl_n;
+    if ((rc = launch_linear(ws.xn, w + lay.off[4], T, D, D, ep, stream)) != TT_OK) return rc;
+    if ((rc = launch_layernorm_rows(ws.xa, w + lay.off[6], w + lay.off[7], nullptr, nullptr,
+                                    ws.vl_n, nullptr, ws.xn, T, D, 1e-5f, stream)) != TT_OK)
+      return rc;
+    ep = EpiArgs{};
+    ep.bias = w + lay.off[9];
+    ep.y = ws.hbuf;
+    ep.ldy = F;
+    ep.mode = TT_EPI_BIAS_GELU;
+    ep.m_dev = ws.vl_n;
+    if ((rc = launch_linear(ws.xn, w + lay.off[8], T, F, D, ep, stream)) != TT_OK) return rc;
+    ep = EpiArgs{};
+    ep.bias = w + lay.off[11];
+    ep.resid = ws.xa;
+    ep.y = ws.xa;
+    ep.ldy = D;
+    ep.mode = TT_EPI_MASKED_RESID;
+    ep.m_dev = ws.vl_n;
+    if ((rc = launch_linear(ws.hbuf, w + lay.off[10], T, D, F, ep, stream)) != TT_OK) return rc;
+  }
+  return launch_layernorm_rows(ws.xa, wts + lay.final_off, wts + lay.final_off + align64(D), mask,
+                               ws.slot, nullptr, nullptr, y, T, D, 1e-5f, stream);
+}
+
 // The forward on a workspace the caller provides (tt_transformer_fwd) or on the library's own
 // scratch array (tt_transformer_fwd_noalloc, which clears the megakernel's counters first).
 int transformer_fwd(const void* weights, const void* x, const uint8_t* mask, void* y,
@@ -291,16 +417,27 @@ int transformer_fwd(const void* weights, const void* x, const uint8_t* mask, voi
   half* q = ws.qkv;
   half* k = ws.qkv + plane;
   half* vt = ws.qkv + 2 * plane;
-  const int32_t* info = nullptr;
-  if (mask != nullptr) {
-    if ((rc = launch_mask_info(mask, ws.info, B, S, stream)) != TT_OK) return rc;
-    info = ws.info;
-  }
   // TT_PLAN_FUSED_LN: LN1 / LN2 are computed inside the QKV / ffn_in tiles (launch_ln_tile), five
   // launches per layer instead of seven.
   const bool fused_ln = resolve_plan(plan, B, S, D, H, F) == TT_PLAN_FUSED_LN;
   if (fused_ln && ((rc = ln_tile_supported(D, 3 * D)) != TT_OK || (rc = ln_tile_supported(D, F)) != TT_OK))
     return rc;
+  const bool packed = mask != nullptr && packs_rows(fused_ln, folds_layernorm(fused_ln, T, D, F),
+                                                    B, S, D, H, F);
+  const int32_t* info = nullptr;
+  if (mask != nullptr) {
+    if ((rc = launch_mask_info(mask, ws.info, B, S, stream, packed ? ws.vl_counts : nullptr)) !=
+        TT_OK)
+      return rc;
+    info = ws.info;
+  }
+  if (packed) {
+    if ((rc = launch_varlen_maps(mask, ws.info, ws.vl_counts, ws.vl_n, ws.row_tok, ws.slot,
+                                 ws.rowmap, ws.pvalid, q, k, vt, B, S, H, hd, stream)) != TT_OK)
+      return rc;
+    return forward_packed(wts, lay, (const half*)x, mask, (half*)y, ws, info, B, S, D, H, F, L,
+                          causal, stream);
+  }
   // Layer-wise plan: LN2 of every layer and LN1 of layers >= 1 are folded into the projection
   // that follows them (lnfold.hip): the producer of the residual stream (out_proj, ffn_out)
   // writes partial row statistics in its epilogue, and the QKV / ffn_in GEMMs multiply the raw

@@ -28,10 +28,23 @@ struct EpiArgs {
   // Producer side (residual modes): partial (mean, M2) slots of the values written, one per
   // stats_width columns (stats_width = linear_stats_width(...)), row stride ln_stride.
   float2* part_out;       // [M][ln_stride] or nullptr
+  // Packed variable-length rows (MFMA tiles only): the live row count is *m_dev (<= the M the
+  // launch is sized for), read on the device, so only the tiles of valid tokens run; and for
+  // TT_EPI_QKV, rowmap[m] = {(b H S + s) hd, b H hd Sp + s} places packed row m, token (b, s), in
+  // the Q / K and V^T planes.
+  const int* m_dev;
+  const int2* rowmap;
 };
 
 int launch_layernorm(const half* x, const half* gamma, const half* beta, const uint8_t* valid,
                      half* y, int rows, int d, float eps, hipStream_t stream);
+// LayerNorm over packed variable-length rows: output row r reads input row in_row[r] (r itself
+// without a map; a negative entry, or valid[r] == 0, writes +0.0), only rows r < *n_dev run (all
+// `rows` without a count), and copy_out, if given, receives the gathered input row as well (+0.0
+// for a negative entry).
+int launch_layernorm_rows(const half* x, const half* gamma, const half* beta, const uint8_t* valid,
+                          const int* in_row, const int* n_dev, half* copy_out, half* y, int rows,
+                          int d, float eps, hipStream_t stream);
 
 int launch_linear(const half* x, const half* w, int m, int n, int k, const EpiArgs& ep,
                   hipStream_t stream);
@@ -45,13 +58,27 @@ bool linear_is_narrow(int m, int n, int k, int mode);
 int launch_pack_derived(half* w, int64_t stride, const int64_t* off, int D, int F, int L,
                         hipStream_t stream);
 
-int launch_mask_info(const uint8_t* mask, int32_t* info, int batch, int seq, hipStream_t stream);
+// info[b] = 1 + last valid position of sequence b, info[B + b] = whether its valid tokens form a
+// prefix; counts (optional) [B] = valid tokens per sequence.
+int launch_mask_info(const uint8_t* mask, int32_t* info, int batch, int seq, hipStream_t stream,
+                     int32_t* counts = nullptr);
+
+// Packed variable-length token maps of a masked batch (varlen.hip has the layout): writes *n_dev
+// = the packed row count, row_tok[r] = b S + s of packed row r (-1 for rows that pad a sequence
+// to 8), slot[b S + s] = its packed row or -1, rowmap[r] (EpiArgs::rowmap), pvalid[r] = whether
+// packed row r is a valid token, and clears the Q / K / V^T entries of the padded tokens that
+// the attention's tiles read (below the sequence's last key tile), which no packed QKV projection
+// writes.  info is the mask_info of the same mask; counts holds its per-sequence valid counts.
+int launch_varlen_maps(const uint8_t* mask, const int32_t* info, int32_t* counts, int32_t* n_dev,
+                       int32_t* row_tok, int32_t* slot, int2* rowmap, uint8_t* pvalid, half* q,
+                       half* k, half* vt, int B, int S, int H, int hd, hipStream_t stream);
 
 // q_prescaled: q holds Q multiplied by attention_q_scale(head_dim) (the forward's QKV epilogue
 // writes it so, EpiArgs::q_scale); otherwise the kernels multiply it when they load it.
 int launch_attention(const half* q, const half* k, const half* vt, const uint8_t* mask,
                      const int32_t* info, half* ctx, int batch, int seq, int heads, int head_dim,
-                     int causal, hipStream_t stream, bool q_prescaled = false);
+                     int causal, hipStream_t stream, bool q_prescaled = false,
+                     const int* out_row = nullptr);
 // hd^-1/2 log2(e): the factor of the scores in the exp2-domain softmax.
 float attention_q_scale(int head_dim);
 int attention_head_dim_supported(int head_dim);

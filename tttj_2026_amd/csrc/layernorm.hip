@@ -10,22 +10,37 @@
 
 namespace tt {
 
+// Packed variable-length rows: output row r reads input row in_row[r] (negative: +0.0), only
+// rows below *n_dev run, and copy_out receives the gathered input row (the residual stream of
+// the first layer).
+struct LnRows {
+  const int* in_row;
+  const int* n_dev;
+  half* copy_out;
+};
+
 template <int NV>
 __global__ __launch_bounds__(256) void layernorm_kernel(const half* __restrict__ x,
                                                         const half* __restrict__ gamma,
                                                         const half* __restrict__ beta,
                                                         const uint8_t* __restrict__ valid,
                                                         half* __restrict__ y, int rows, int d,
-                                                        float eps) {
+                                                        float eps, LnRows pk) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
+  if (pk.n_dev != nullptr) rows = min(rows, *pk.n_dev);
   if (row >= rows) return;
   const int nch = d >> 3;
   const size_t base = (size_t)row * d;
-  if (valid != nullptr && valid[row] == 0) {
-    for (int c = lane; c < nch; c += 64) *(uint4*)(y + base + 8 * c) = make_uint4(0, 0, 0, 0);
+  const int src = pk.in_row != nullptr ? pk.in_row[row] : row;
+  if ((valid != nullptr && valid[row] == 0) || src < 0) {
+    for (int c = lane; c < nch; c += 64) {
+      *(uint4*)(y + base + 8 * c) = make_uint4(0, 0, 0, 0);
+      if (pk.copy_out != nullptr) *(uint4*)(pk.copy_out + base + 8 * c) = make_uint4(0, 0, 0, 0);
+    }
     return;
   }
+  const size_t sbase = (size_t)src * d;
   // The row and the affine chunks are loaded together, so gamma / beta do not add a memory round
   // trip after the reductions (the kernel is latency-bound for small row counts).
   half8 v[NV], g[NV], bt[NV];
@@ -33,7 +48,8 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const half* __restrict__
   for (int i = 0; i < NV; ++i) {
     const int c = lane + 64 * i;
     if (c < nch) {
-      v[i] = *(const half8*)(x + base + 8 * c);
+      v[i] = *(const half8*)(x + sbase + 8 * c);
+      if (pk.copy_out != nullptr) *(half8*)(pk.copy_out + base + 8 * c) = v[i];
       g[i] = *(const half8*)(gamma + 8 * c);
       bt[i] = *(const half8*)(beta + 8 * c);
     }
@@ -74,24 +90,32 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const half* __restrict__
   }
 }
 
-int launch_layernorm(const half* x, const half* gamma, const half* beta, const uint8_t* valid,
-                     half* y, int rows, int d, float eps, hipStream_t stream) {
+int launch_layernorm_rows(const half* x, const half* gamma, const half* beta, const uint8_t* valid,
+                          const int* in_row, const int* n_dev, half* copy_out, half* y, int rows,
+                          int d, float eps, hipStream_t stream) {
   TT_REQUIRE(rows >= 0 && d > 0 && d % 8 == 0 && d <= 8192,
              "layernorm: need d %% 8 == 0 and 0 < d <= 8192 (got d=%d)", d);
   if (rows == 0) return TT_OK;
   const dim3 grid((rows + 3) / 4), block(256);
   const int nv = (d / 8 + 63) / 64;
+  const LnRows pk{in_row, n_dev, copy_out};
   if (nv <= 1)
-    hipLaunchKernelGGL(layernorm_kernel<1>, grid, block, 0, stream, x, gamma, beta, valid, y, rows, d, eps);
+    hipLaunchKernelGGL(layernorm_kernel<1>, grid, block, 0, stream, x, gamma, beta, valid, y, rows, d, eps, pk);
   else if (nv <= 2)
-    hipLaunchKernelGGL(layernorm_kernel<2>, grid, block, 0, stream, x, gamma, beta, valid, y, rows, d, eps);
+    hipLaunchKernelGGL(layernorm_kernel<2>, grid, block, 0, stream, x, gamma, beta, valid, y, rows, d, eps, pk);
   else if (nv <= 4)
-    hipLaunchKernelGGL(layernorm_kernel<4>, grid, block, 0, stream, x, gamma, beta, valid, y, rows, d, eps);
+    hipLaunchKernelGGL(layernorm_kernel<4>, grid, block, 0, stream, x, gamma, beta, valid, y, rows, d, eps, pk);
   else if (nv <= 8)
-    hipLaunchKernelGGL(layernorm_kernel<8>, grid, block, 0, stream, x, gamma, beta, valid, y, rows, d, eps);
+    hipLaunchKernelGGL(layernorm_kernel<8>, grid, block, 0, stream, x, gamma, beta, valid, y, rows, d, eps, pk);
   else
-    hipLaunchKernelGGL(layernorm_kernel<16>, grid, block, 0, stream, x, gamma, beta, valid, y, rows, d, eps);
+    hipLaunchKernelGGL(layernorm_kernel<16>, grid, block, 0, stream, x, gamma, beta, valid, y, rows, d, eps, pk);
   return launch_status("layernorm_kernel");
+}
+
+int launch_layernorm(const half* x, const half* gamma, const half* beta, const uint8_t* valid,
+                     half* y, int rows, int d, float eps, hipStream_t stream) {
+  return launch_layernorm_rows(x, gamma, beta, valid, nullptr, nullptr, nullptr, y, rows, d, eps,
+                               stream);
 }
 
 }  // namespace tt

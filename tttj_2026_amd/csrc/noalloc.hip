@@ -19,6 +19,13 @@ static __device__ __align__(256) char scratch[kScratchBytes];
 static constexpr int kMaxDevices = 64;
 static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[kMaxDevices];
+// Shape of the latest megakernel-plan call on each device: its error word sits at a
+// shape-dependent offset of the array and stays there until the next call clears it.
+struct MegaShape {
+  bool valid;
+  int B, S, D, F, L;
+};
+static MegaShape g_last_mega[kMaxDevices];
 
 static int scratch_address(void** out) {
   int dev = 0;
@@ -57,7 +64,33 @@ extern "C" int tt_transformer_fwd_noalloc(const void* weights, const void* x, co
              (long long)need, kScratchBytes);
   void* ws = nullptr;
   if ((rc = scratch_address(&ws)) != TT_OK) return rc;
-  return transformer_fwd(weights, x, mask, y, ws, (int64_t)kScratchBytes, batch, seq, d_model,
-                         num_heads, ffn_dim, num_layers, causal, plan, true, stream);
+  int dev = 0;
+  TT_HIP(hipGetDevice(&dev));
+  const bool mega =
+      tt_resolve_plan(batch, seq, d_model, num_heads, ffn_dim, plan) == TT_PLAN_MEGAKERNEL;
+  rc = transformer_fwd(weights, x, mask, y, ws, (int64_t)kScratchBytes, batch, seq, d_model,
+                       num_heads, ffn_dim, num_layers, causal, plan, true, stream);
+  std::lock_guard<std::mutex> guard(g_scratch_mu);
+  g_last_mega[dev] = MegaShape{mega && rc == TT_OK, batch, seq, d_model, ffn_dim, num_layers};
+  return rc;
+}
+
+// Health of the latest tt_transformer_fwd_noalloc call on the current device: its megakernel
+// error word (the next call's counter reset clears it, so it is read before that call).
+extern "C" int tt_noalloc_status(int* status, void* stream) {
+  TT_REQUIRE(status != nullptr, "noalloc_status: null output");
+  int dev = 0;
+  TT_HIP(hipGetDevice(&dev));
+  TT_REQUIRE(dev >= 0 && dev < kMaxDevices, "noalloc_status: device %d out of range", dev);
+  MegaShape m;
+  void* ws = nullptr;
+  {
+    std::lock_guard<std::mutex> guard(g_scratch_mu);
+    m = g_last_mega[dev];
+    ws = g_scratch_ptr[dev];
+  }
+  *status = 0;
+  if (!m.valid || ws == nullptr) return TT_OK;
+  return megakernel_status((const char*)ws, m.B, m.S, m.D, m.F, m.L, status, (hipStream_t)stream);
 }
 

@@ -110,10 +110,13 @@ def mask_info(mask: Optional[torch.Tensor], batch: int, seq: int, device) -> tor
 
 
 def attention(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, mask: Optional[torch.Tensor],
-              causal: bool, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+              causal: bool, out: Optional[torch.Tensor] = None,
+              prescaled: bool = False) -> torch.Tensor:
     """q, k [B,H,S,hd], vt [B,H,hd,Sp] (views from qkv_projection) -> ctx [B,S,H*hd].
 
     `out`, if given, is a contiguous fp16 [B,S,H*hd] tensor on the same device that receives ctx.
+    `prescaled`: q already holds Q * hd^-1/2 * log2(e) (the forward's own Q,
+    tt_attention_fwd_prescaled); otherwise the kernel applies the factor when it loads q.
     """
     b, h, s, hd = q.shape
     if k.shape != q.shape or vt.shape[:3] != (b, h, hd) or vt.shape[3] != (s + 63) // 64 * 64:
@@ -130,8 +133,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, mask: Optional
         raise ValueError("out must be a contiguous fp16 [B,S,H*hd] tensor on q's device")
     else:
         ctx = out
-    rc = _lib.load().tt_attention_fwd(q.data_ptr(), k.data_ptr(), vt.data_ptr(), _ptr(mask),
-                                      _ptr(info), ctx.data_ptr(), b, s, h, hd, int(causal),
-                                      _stream(q))
+    fn = _lib.load().tt_attention_fwd_prescaled if prescaled else _lib.load().tt_attention_fwd
+    rc = fn(q.data_ptr(), k.data_ptr(), vt.data_ptr(), _ptr(mask), _ptr(info), ctx.data_ptr(), b,
+            s, h, hd, int(causal), _stream(q))
     _lib.check(rc, "tt_attention_fwd")
     return ctx

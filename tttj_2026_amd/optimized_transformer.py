@@ -169,6 +169,8 @@ class OptimizedTransformer(nn.Module):
             OrderedDict()
         self._nbytes: Dict[Tuple[int, int, int], int] = {}
         self.last_workspace: Optional[torch.Tensor] = None
+        self.last_mask: Optional[torch.Tensor] = None
+        self._pinned = set()  # megakernel workspaces a captured graph holds
 
     def prepare(self) -> None:
         check_supported(self.config)
@@ -206,7 +208,11 @@ class OptimizedTransformer(nn.Module):
             self._attach(entry, batch, seq)
         self._mega[key] = entry  # most recently used last
         while len(self._mega) > MEGA_WORKSPACES_KEPT:
-            self._mega.popitem(last=False)
+            # least recently used first; a workspace a captured graph replays on is never dropped
+            victim = next((k for k in self._mega if k not in self._pinned), None)
+            if victim is None:
+                break
+            self._detach(self._mega.pop(victim), victim[0], victim[1])
         return entry
 
     @staticmethod
@@ -220,6 +226,27 @@ class OptimizedTransformer(nn.Module):
             ws.data_ptr(), ws.numel(), batch, seq, cfg.d_model, cfg.num_heads, cfg.ffn_dim,
             cfg.num_layers, status.data_ptr(),
             torch.cuda.current_stream(ws.device).cuda_stream), "tt_megakernel_attach_status")
+
+    def _detach(self, entry, batch, seq) -> None:
+        """Before a workspace and its pinned status word are dropped: detach the word, ordered
+        after the workspace's last launch (whose final workgroup writes through the attached
+        address), and wait for that point, so the freed word is never written."""
+        ws, _, _ = entry
+        cfg = self.config
+        stream = torch.cuda.current_stream(ws.device)
+        _lib.check(self._lib.tt_megakernel_attach_status(
+            ws.data_ptr(), ws.numel(), batch, seq, cfg.d_model, cfg.num_heads, cfg.ffn_dim,
+            cfg.num_layers, None, stream.cuda_stream), "tt_megakernel_attach_status")
+        stream.synchronize()
+
+    def pin_workspace(self, batch: int, seq: int, device_index: int):
+        """Keep the megakernel workspace of (batch, seq) and its status word for good (a captured
+        graph replays on them) and return that entry; None for other plans."""
+        key = (batch, seq, device_index)
+        entry = self._mega.get(key)
+        if entry is not None:
+            self._pinned.add(key)
+        return entry
 
     def _check_mega_health(self, entry, batch, seq) -> None:
         """Raise MegakernelWaitError if an earlier launch on this workspace reported a wait that
@@ -305,6 +332,7 @@ class OptimizedTransformer(nn.Module):
         if plan == PLAN_MEGAKERNEL:
             self._check_mega_health(self._mega[(batch, seq, x.device.index or 0)], batch, seq)
         self.last_workspace = ws
+        self.last_mask = valid_token_mask
         stream = torch.cuda.current_stream(x.device).cuda_stream
         rc = self._lib.tt_transformer_fwd(
             self.packed_weights.data_ptr(), x.data_ptr(), mask_ptr, y.data_ptr(), ws.data_ptr(),
@@ -341,7 +369,17 @@ class OptimizedTransformer(nn.Module):
         k = qkv[plane:2 * plane].view(batch, h, seq, hd)
         v = qkv[2 * plane:].view(batch, h, hd, sp)[..., :seq].transpose(-1, -2)
         ctx = None if oc < 0 else view(oc, t * d).view(batch, seq, d)
-        hidden = view(oh, t * f).view(batch, seq, f)
+        hidden = view(oh, t * f).view(t, f)
+        mask = self.last_mask
+        if mask is not None and plan != PLAN_MEGAKERNEL and _lib.forward_packs_rows(
+                batch, seq, d, h, f, plan):
+            # packed variable-length rows: scatter the valid tokens' rows back to [B, S, F]
+            rows = torch.tensor(_lib.packed_row_tokens(mask.cpu(), seq), dtype=torch.long)
+            keep = rows >= 0
+            full = torch.zeros(t, f, dtype=hidden.dtype, device=hidden.device)
+            full[rows[keep].to(hidden.device)] = hidden[:rows.numel()][keep.to(hidden.device)]
+            hidden = full
+        hidden = hidden.view(batch, seq, f)
         return {"q": q, "k": k, "v": v, "ctx": ctx, "hidden": hidden}
 
 
@@ -374,6 +412,7 @@ class GraphedOptimizedTransformer(nn.Module):
         self._static_mask: Optional[torch.Tensor] = None
         self._static_output: Optional[torch.Tensor] = None
         self._static_workspace: Optional[torch.Tensor] = None
+        self._static_entry = None
 
     @staticmethod
     def _signature(x: torch.Tensor, mask: Optional[torch.Tensor]):
@@ -398,8 +437,11 @@ class GraphedOptimizedTransformer(nn.Module):
         with torch.cuda.graph(graph), torch.inference_mode():
             out = self.module(x, valid_token_mask)
         # the graph replays on this workspace: keep it alive even if the module later grows or
-        # drops its own buffers
+        # drops its own buffers; a megakernel workspace is pinned in the module together with
+        # the status word its launches write (never evicted, never freed while replays run)
         self._static_workspace = self.module.last_workspace
+        b, s = x.shape[:2]
+        self._static_entry = self.module.pin_workspace(b, s, dev.index if dev.index is not None else 0)
         self._graph = graph
         self._key = self._signature(x, valid_token_mask)
         self._static_input, self._static_mask, self._static_output = x, valid_token_mask, out
