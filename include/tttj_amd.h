@@ -181,8 +181,7 @@ int tt_linear_fwd(const void* x, const void* w, const void* bias, const void* re
 /* Test hook: force tile configuration `index` (0: 256x256 on 8 waves, 1: 256x128, 2: 128x128,
  * 3: 128x64, 4: 64x64, 5: 32x32 narrow tiles with K split over the block's waves; 6-9: 128x256,
  * 128x128, 128x64, 256x128 staged through registers; 10: 256x128 on 8 waves with a three-stage
- * K ring; 11, 12: 256x256 / 256x128 on 8 waves with 32-deep K stages in a 4- / 6-stage ring) for
- * every later GEMM whose N it divides; -1 restores the automatic choice.  Process
+ * K ring) for every later GEMM whose N it divides; -1 restores the automatic choice.  Process
  * wide, not thread-safe.  No counterpart in the reference (its tile choices are compile-time
  * constants per case, kernels/fused_megakernel.py:121-171). */
 int tt_gemm_tile_override(int index);

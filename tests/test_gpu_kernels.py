@@ -55,7 +55,7 @@ GEMM_SHAPES = [(64, 768, 256), (100, 64, 64), (512, 1024, 256), (4096, 1536, 512
                (130, 256, 192)]
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12])
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
 def test_linear_bias_all_tiles(device, m, n, k, tile):
     if tile >= 0 and m * n * k > 2 ** 31:
@@ -121,7 +121,7 @@ def _padded_rows(m, seed):
     return v
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 2, 4, 5, 6, 7, 8, 9, 10, 11, 12])
+@pytest.mark.parametrize("tile", [-1, 0, 2, 4, 5, 6, 7, 8, 9, 10])
 @pytest.mark.parametrize("mode", ["bias", "gelu", "resid_masked", "masked_resid"])
 @pytest.mark.parametrize("m,n,k,seq", [(1000, 512, 256, 0), (4096, 1024, 512, 0),
                                        (4096, 1024, 512, 512), (8192, 256, 256, 1024)])
@@ -163,7 +163,7 @@ def test_linear_masked_rows(device, m, n, k, seq, mode, tile):
         assert _bits_zero(got[~v])
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 2, 4, 5, 6, 7, 8, 9, 10, 11, 12])
+@pytest.mark.parametrize("tile", [-1, 0, 2, 4, 5, 6, 7, 8, 9, 10])
 @pytest.mark.parametrize("b,s,d,h", [(4, 256, 512, 8), (3, 100, 256, 4), (2, 1024, 1024, 16),
                                      (4, 100, 32, 4), (2, 130, 96, 3), (3, 128, 128, 16),
                                      (2, 64, 1024, 4), (2, 72, 128, 1), (5, 3, 64, 2),

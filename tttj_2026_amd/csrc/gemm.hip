@@ -145,16 +145,13 @@ __device__ void fill_padded_tile(const EpiArgs& ep, int M, int m0, int n0) {
 // 128 x 128 share a CU (one's epilogue runs beside the other's main loop); an 8-wave block puts two
 // waves on every SIMD by itself.
 // K stages in the LDS ring: three for the 8-wave 256 x 128 direct-copy tile (3 x 48 KiB), so a
-// stage's copies are issued two stages before it is read; two for every other 64-deep tile.  The
-// 32-deep ring (PATH = 2, 8 waves) holds four stages of a 256 x 256 tile (4 x 32 KiB) or six of a
-// 256 x 128 tile (6 x 24 KiB).
+// stage's copies are issued two stages before it is read; two for every other tile.
 constexpr int gemm_stages(int bm, int bn, int path, int nw) {
-  if (path == 2) return bm * bn >= 256 * 256 ? 4 : 6;
   return (path == 0 && nw == 8 && bm * bn <= 256 * 128) ? 3 : 2;
 }
-// LDS row stride (halfs) of a staged operand row: 64-deep K stages in 128-byte rows (direct
-// copies, XOR-swizzled) or 144-byte padded rows (register path), 32-deep stages in 64-byte rows.
-constexpr int gemm_ldr(int path) { return path == 1 ? kBK + 8 : (path == 2 ? 32 : kBK); }
+// LDS row stride (halfs) of a staged operand row: 128-byte rows (direct copies, XOR-swizzled) or
+// 144-byte padded rows (register path).
+constexpr int gemm_ldr(int path) { return path == 1 ? kBK + 8 : kBK; }
 
 template <int BM, int BN, int MODE, int PATH, int NW = 4>
 __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1) void gemm_kernel(
@@ -171,7 +168,6 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1)
   constexpr int LDR = gemm_ldr(PATH);
   constexpr int STAGE = ROWS * LDR;   // halfs per stage
   static_assert(PATH != 1 || NW == 4, "the register path is laid out for 4 waves");
-  static_assert(PATH != 2 || NW == 8, "the 32-deep ring is laid out for 8 waves");
   constexpr int XL = BM / (8 * NW);   // X copies per wave per stage (8 rows each)
   constexpr int WL = BN / (8 * NW);   // W copies per wave per stage
   constexpr int NL = XL + WL;
@@ -372,7 +368,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1)
     }
     wait_vmcnt<0>();  // the re-read copies past the end land before the epilogue reuses LDS
 
-  } else if constexpr (PATH == 1) {
+  } else {
     // Register path.  Thread t moves chunk t % 8 of rows t / 8 + 32 i (i < RX: X rows, then W
     // rows) of every stage.  The buffers start at the block's first X / W row, so offsets stay
     // below BM * K and BN * K; X rows past M are clamped to M - 1 (valid memory whose results are
@@ -460,118 +456,6 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1)
       body(kt + 1, sa);
     }
     if (kt < nk) body(kt, sb);
-  } else {
-    // 32-deep K stages in an NS-stage LDS ring (8 waves).  A stage is BM + BN rows of 64 bytes;
-    // one global -> LDS copy fills 16 rows (1 KiB), lane l writing row l / 4, physical chunk l % 4.
-    // Chunks are XOR-swizzled with bits 2-3 of the row (physical = logical ^ ((r >> 2) & 3)), so
-    // the 16 rows one ds_read_b128 phase reads land in 16 different bank groups; the swizzle is
-    // applied on the global side (lane l fetches logical chunk (l & 3) ^ ((l >> 4) & 3)).
-    //
-    // Stage k is computed in two halves around one barrier B_k: k-step 0 (fragments read during
-    // the previous stage) with the reads of k-step 1, then B_k, then k-step 1 with the reads of
-    // the next stage's k-step 0.  So no MFMA waits for a fragment read issued after a barrier,
-    // and the MFMAs a wave issues just before B_k keep its SIMD busy while it waits there.
-    //  * Every read of stage s is issued before B_s ends... its k-step-1 reads before B_s and its
-    //    k-step-0 reads after B_{s-1}; all are consumed by stage s's MFMAs, so each wave's reads of
-    //    stage s have completed when it arrives at B_{s+1}: stage s's buffer is free after B_{s+1}.
-    //  * Copies of stage t go to buffer t % NS (free after B_{t-NS+1}) in two batches: B1 in the
-    //    second half of stage t-NS+1, B2 in the first half of stage t-NS+2.  Each wave waits for
-    //    its own copies of stage k+1 before B_k (vmcnt <= the copies of stages k+2 .. k+NS-2 that
-    //    were issued after them; loads complete in issue order), and B_k makes every wave's copies
-    //    of stage k+1 visible before its first reads.  A copy thus has at least NS - 3 stages to
-    //    land, and each wave issues one copy every few MFMAs instead of a burst per stage: a burst
-    //    fills the CU's copy queue, and a wave blocked at a copy issues no MFMAs.
-    //  * Copies of stages past the last re-read it into a buffer no remaining stage reads, so
-    //    every stage body is the same basic block (no branch between its interleaved groups).
-    constexpr int BK2 = 32;
-    constexpr int NCOPY = (BM + BN) / 16;       // 1 KiB copies per stage
-    constexpr int CPS = NCOPY / NW;             // copies per wave per stage
-    constexpr int XI = BM / (16 * NW);          // the first XI copies of a wave are X rows
-    constexpr int B1 = (CPS + 1) / 2, B2 = CPS - B1;
-    static_assert(NCOPY % NW == 0 && BM % (16 * NW) == 0, "copy split");
-    static_assert(NS >= 4, "a copy needs at least one whole stage to land");
-    const int nk = K / BK2;
-    const int lrow = lane >> 2, lch = (lane & 3) ^ ((lane >> 4) & 3);
-    const half* Xb = X + (size_t)m0 * K;
-    const half* Wb = W + (size_t)n0 * K;
-    int src_off[CPS];
-#pragma unroll
-    for (int i = 0; i < CPS; ++i) {
-      const int r = 16 * (wave + NW * i) + lrow;   // row of the stage: X rows, then W rows
-      if (i < XI) src_off[i] = min(r, M - 1 - m0) * K + lch * 8;
-      else src_off[i] = (r - BM) * K + lch * 8;
-    }
-    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    auto copy = [&](int i, int kt, half* stage) {
-      const half* base = ((i < XI) ? Xb : Wb) + min(kt, nk - 1) * BK2;
-      lds_copy16(base + (uint32_t)src_off[i], stage + (wave_u + NW * i) * 16 * BK2);
-    };
-    // Fragment of k-step kk: lane l reads row l % 32 of a 32-row block at logical chunk
-    // 2 kk + l / 32; the block starts on a multiple of 32 rows, so the swizzle term is (l >> 2) & 3.
-    const int fsw = (lane >> 2) & 3;
-    const int pcs[2] = {(fhi) ^ fsw, (2 + fhi) ^ fsw};
-    auto frags2 = [&](int set, const half* st) {
-      const int pc = pcs[set];
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-        af[set][i] = *(const half8*)(st + (BM + wn * WN + i * 32 + frow) * BK2 + pc * 8);
-#pragma unroll
-      for (int j = 0; j < FM; ++j)
-        bf[set][j] = *(const half8*)(st + (wm * WM + j * 32 + frow) * BK2 + pc * 8);
-    };
-    // One half stage: the FN x FM MFMAs of fragment set `set`, with the FN + FM fragment reads
-    // issued before it (set `1 - set`) and `nc` copies spread over the MFMAs.
-    auto interleave = [&](int nc) {
-#pragma unroll
-      for (int t = 0; t < FN * FM; ++t) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                       // MFMA
-        if (t < FN + FM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // DS read
-        if ((t * nc) / (FN * FM) != ((t + 1) * nc) / (FN * FM))
-          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                     // copy
-      }
-    };
-    auto mma = [&](int set) {
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-#pragma unroll
-        for (int j = 0; j < FM; ++j) acc[i][j] = mfma32x32x16(af[set][i], bf[set][j], acc[i][j]);
-    };
-    auto buf = [&](int s) { return lds + (s % NS) * STAGE; };
-    // Stage k (compile-time ring slot u = k % NS): batch 2 of stage k + NS - 2 in the first half,
-    // batch 1 of stage k + NS - 1 in the second.
-    auto stage2 = [&](int k, int u) {
-      __builtin_amdgcn_sched_barrier(0);
-      frags2(1, buf(u));
-#pragma unroll
-      for (int c = 0; c < B2; ++c) copy(B1 + c, k + NS - 2, buf(u + NS - 2));
-      mma(0);
-      interleave(B2);
-      __builtin_amdgcn_sched_barrier(0);
-      wait_vmcnt<(NS - 3) * CPS>();
-      raw_barrier();
-      frags2(0, buf(u + 1));
-#pragma unroll
-      for (int c = 0; c < B1; ++c) copy(c, k + NS - 1, buf(u + NS - 1));
-      mma(1);
-      interleave(B1);
-      __builtin_amdgcn_sched_barrier(0);
-    };
-    // Prologue: stages 0 .. NS - 3 whole and batch 1 of stage NS - 2; then stage 0 is waited for.
-#pragma unroll
-    for (int s = 0; s < NS - 2; ++s)
-#pragma unroll
-      for (int i = 0; i < CPS; ++i) copy(i, s, buf(s));
-#pragma unroll
-    for (int c = 0; c < B1; ++c) copy(c, NS - 2, buf(NS - 2));
-    wait_vmcnt<(NS - 3) * CPS + B1>();
-    raw_barrier();
-    frags2(0, buf(0));
-    for (int k = 0; k < nk; k += NS) {
-#pragma unroll
-      for (int u = 0; u < NS; ++u)
-        if (k + u < nk) stage2(k + u, u);
-    }
-    wait_vmcnt<0>();  // the re-read copies past the end land before the epilogue reuses LDS
   }
 
   // ---- Epilogue ----
@@ -1048,8 +932,6 @@ static int run_mode(int tile, const half* x, const half* w, int m, int n, int k,
     case 8: return run_tile<128, 64, MODE, 1>(x, w, m, n, k, ep, stream);
     case 9: return run_tile<256, 128, MODE, 1>(x, w, m, n, k, ep, stream);
     case 10: return run_tile<256, 128, MODE, 0, 8>(x, w, m, n, k, ep, stream);
-    case 11: return run_tile<256, 256, MODE, 2, 8>(x, w, m, n, k, ep, stream);
-    case 12: return run_tile<256, 128, MODE, 2, 8>(x, w, m, n, k, ep, stream);
     default: return run_tile<64, 64, MODE, 0>(x, w, m, n, k, ep, stream);
   }
 }
@@ -1059,7 +941,7 @@ static int run_mode(int tile, const half* x, const half* w, int m, int n, int k,
 // register path; index 10: 256 x 128 on 8 waves with a three-stage ring
 static const TileCfg kTiles[] = {{256, 256}, {256, 128}, {128, 128}, {128, 64}, {64, 64},
                                  {32, 32},   {128, 256}, {128, 128}, {128, 64}, {256, 128},
-                                 {256, 128}, {256, 256}, {256, 128}};
+                                 {256, 128}};
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
 static int g_tile_override = -1;  // test hook: force one tile configuration
