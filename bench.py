@@ -341,6 +341,101 @@ def bench_reference_cases(dev, rounds, eager):
             "gpu": torch.cuda.get_device_name(dev)}
 
 
+def forward_runs(name, dev, steps, warmup):
+    """The workload's own forward (the plan its shape resolves to), `steps` times after `warmup`:
+    for rocprofv3 counter runs over exactly the kernels a forward of this workload launches."""
+    cfg = WORKLOADS[name].config
+    x16, mask = workload_inputs(name)
+    opt = make_optimized_transformer(build_model(cfg).half().to(dev).eval())
+    xd = x16.to(dev)
+    md = None if mask is None else mask.to(dev)
+    plan = _lib.resolve_plan(cfg.batch_size, cfg.seq_len, cfg.d_model, cfg.num_heads, cfg.ffn_dim,
+                             opt.plan)
+    with torch.inference_mode():
+        for _ in range(warmup):
+            opt(xd, md)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            opt(xd, md)
+        torch.cuda.synchronize()
+    return {"workload": name, "plan": plan, "steps": steps,
+            "ms_per_forward": (time.perf_counter() - t0) * 1e3 / max(steps, 1),
+            "packed_rows": bool(md is not None and _lib.forward_packs_rows(
+                cfg.batch_size, cfg.seq_len, cfg.d_model, cfg.num_heads, cfg.ffn_dim, plan))}
+
+
+MEGA_KINDS = ("qkv", "attention", "out_proj", "ffn_in", "ffn_out")
+
+
+def megakernel_trace_summary(name, dev, reps=20):
+    """Per-task trace of the persistent megakernel (forward_traced) on the workload's shape, per
+    layer and task kind (stage): the task count, the median run time (dependencies met -> end)
+    and, relative to the launch's first task start, when the stage's first and median task had
+    its dependencies met and when its last task ended (the critical path); also how busy the
+    workgroups were.  Medians over `reps` launches; times in us (the trace clock is 100 MHz).
+    Task numbering per layer: QKV (row blocks x 3D/64 tiles), attention (B x H x query blocks of
+    128), out_proj (row blocks x D/64), ffn_in (row blocks x F/64), ffn_out (row blocks x D/64 x K
+    splits), then one final LayerNorm task per row block (csrc/megakernel.hip,
+    megakernel_tasks)."""
+    cfg = WORKLOADS[name].config
+    x16, mask = workload_inputs(name)
+    opt = make_optimized_transformer(build_model(cfg).half().to(dev).eval())
+    xd = x16.to(dev)
+    md = None if mask is None else mask.to(dev)
+    B, S, D, H, F, L = (cfg.batch_size, cfg.seq_len, cfg.d_model, cfg.num_heads, cfg.ffn_dim,
+                        cfg.num_layers)
+    nrb = B * -(-S // 64)
+    nqb = -(-S // 128)
+    with torch.inference_mode():
+        traces = [opt.forward_traced(xd, md)[1].tolist() for _ in range(reps)]
+    ntask = len(traces[0])
+    per_layer = (ntask - nrb) // L
+    counts = [nrb * 3 * D // 64, B * H * nqb, nrb * D // 64, nrb * F // 64]
+    counts.append(per_layer - sum(counts))
+    kind_of = []
+    for k, c in enumerate(counts):
+        kind_of += [k] * c
+
+    def stage(task):
+        if task >= L * per_layer:
+            return (L, "final_norm")
+        return (task // per_layer, MEGA_KINDS[kind_of[task % per_layer]])
+
+    spans, busy = [], []
+    acc = {}
+    for t in traces:
+        t0 = min(r[1] for r in t)
+        t1 = max(r[3] for r in t)
+        spans.append((t1 - t0) / 100.0)
+        wgs = len({r[0] >> 32 for r in t})
+        busy.append(sum(r[3] - r[1] for r in t) / (wgs * (t1 - t0)))
+        per = {}
+        for task, r in enumerate(t):
+            per.setdefault(stage(task), []).append(r)
+        for key, rs in per.items():
+            ready = sorted((r[2] - t0) / 100.0 for r in rs)
+            a = acc.setdefault(key, {"run": [], "first_ready": [], "ready": [], "last_end": []})
+            a["run"] += [(r[3] - r[2]) / 100.0 for r in rs]
+            a["first_ready"].append(ready[0])
+            a["ready"].append(statistics.median(ready))
+            a["last_end"].append(max((r[3] - t0) / 100.0 for r in rs))
+    rows = []
+    for (layer, kind) in sorted(acc, key=lambda k: (k[0], MEGA_KINDS.index(k[1])
+                                                     if k[1] in MEGA_KINDS else 9)):
+        a = acc[(layer, kind)]
+        rows.append({"layer": layer if kind != "final_norm" else -1, "kind": kind,
+                     "tasks": len(a["run"]) // reps,
+                     "run_us_p50": statistics.median(a["run"]),
+                     "first_ready_us": statistics.median(a["first_ready"]),
+                     "ready_us_p50": statistics.median(a["ready"]),
+                     "last_end_us": statistics.median(a["last_end"])})
+    return {"workload": name, "tasks": ntask,
+            "workgroups": len({r[0] >> 32 for r in traces[-1]}),
+            "span_us_p50": statistics.median(spans), "busy_frac_p50": statistics.median(busy),
+            "per_layer_kind": rows}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -351,10 +446,13 @@ def main() -> int:
     ap.add_argument("--rounds", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-eager", action="store_true")
-    ap.add_argument("--mode", default="full", choices=("full", "kernels", "cases"),
+    ap.add_argument("--mode", default="full",
+                    choices=("full", "kernels", "forward", "trace", "cases"),
                     help="kernels: only run each kernel of one layer (and a copy of known size) "
-                         "a few times, for rocprofv3 counter runs; cases: time the reference's "
-                         "own 14-case shape table against eager fp16 (one JSON line)")
+                         "a few times, for rocprofv3 counter runs; forward: only run the "
+                         "workload's own forward --steps times; trace: per-task summary of the "
+                         "megakernel's trace on the workload's shape; cases: time the "
+                         "reference's own 14-case shape table against eager fp16 (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -369,6 +467,13 @@ def main() -> int:
     cfg = WORKLOADS[name].config
     if args.mode == "cases":
         print(json.dumps(bench_reference_cases(dev, args.rounds, not args.no_eager)))
+        return 0
+    if args.mode == "forward":
+        copy_calibration(dev)
+        print(json.dumps(forward_runs(name, dev, args.steps, args.warmup)))
+        return 0
+    if args.mode == "trace":
+        print(json.dumps(megakernel_trace_summary(name, dev)))
         return 0
     if args.mode == "kernels":
         copy_calibration(dev)
