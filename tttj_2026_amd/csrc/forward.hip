@@ -425,18 +425,16 @@ int transformer_fwd(const void* weights, const void* x, const uint8_t* mask, voi
   const bool packed = mask != nullptr && packs_rows(fused_ln, folds_layernorm(fused_ln, T, D, F),
                                                     B, S, D, H, F);
   const int32_t* info = nullptr;
-  if (mask != nullptr) {
-    if ((rc = launch_mask_info(mask, ws.info, B, S, stream, packed ? ws.vl_counts : nullptr)) !=
-        TT_OK)
-      return rc;
-    info = ws.info;
-  }
   if (packed) {
-    if ((rc = launch_varlen_maps(mask, ws.info, ws.vl_counts, ws.vl_n, ws.row_tok, ws.slot,
+    if ((rc = launch_varlen_prep(mask, ws.info, ws.vl_counts, ws.vl_n, ws.row_tok, ws.slot,
                                  ws.rowmap, ws.pvalid, q, k, vt, B, S, H, hd, stream)) != TT_OK)
       return rc;
-    return forward_packed(wts, lay, (const half*)x, mask, (half*)y, ws, info, B, S, D, H, F, L,
+    return forward_packed(wts, lay, (const half*)x, mask, (half*)y, ws, ws.info, B, S, D, H, F, L,
                           causal, stream);
+  }
+  if (mask != nullptr) {
+    if ((rc = launch_mask_info(mask, ws.info, B, S, stream)) != TT_OK) return rc;
+    info = ws.info;
   }
   // Layer-wise plan: LN2 of every layer and LN1 of layers >= 1 are folded into the projection
   // that follows them (lnfold.hip): the producer of the residual stream (out_proj, ffn_out)

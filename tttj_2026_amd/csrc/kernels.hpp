@@ -72,6 +72,12 @@ int launch_mask_info(const uint8_t* mask, int32_t* info, int batch, int seq, hip
 int launch_varlen_maps(const uint8_t* mask, const int32_t* info, int32_t* counts, int32_t* n_dev,
                        int32_t* row_tok, int32_t* slot, int2* rowmap, uint8_t* pvalid, half* q,
                        half* k, half* vt, int B, int S, int H, int hd, hipStream_t stream);
+// launch_mask_info (with counts) and launch_varlen_maps in one launch, one block per sequence
+// (each scans the masks of the sequences before it); the two launches for batches whose scan
+// would be long.
+int launch_varlen_prep(const uint8_t* mask, int32_t* info, int32_t* counts, int32_t* n_dev,
+                       int32_t* row_tok, int32_t* slot, int2* rowmap, uint8_t* pvalid, half* q,
+                       half* k, half* vt, int B, int S, int H, int hd, hipStream_t stream);
 
 // q_prescaled: q holds Q multiplied by attention_q_scale(head_dim) (the forward's QKV epilogue
 // writes it so, EpiArgs::q_scale); otherwise the kernels multiply it when they load it.
