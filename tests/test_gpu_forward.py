@@ -122,6 +122,46 @@ def test_packed_rows_masks(device, kind, b, s, d, h, f, causal):
         assert torch.equal(y0, y1)
 
 
+# More than 2^20 tokens: the packed-row set-up takes its three-launch path (mask summary, maps,
+# V^T clear) instead of the one-launch kernel.  Packed against padded forward bitwise, padded rows
+# +0.0, and a few sequences against the oracle (sequences are independent, so each is checked on
+# its own).
+@pytest.mark.timeout(600)
+def test_packed_rows_long_batch(device):
+    from tttj_2026_amd import _lib
+    b, s, d, h, f = 2048, 520, 64, 1, 64
+    assert b * s > (1 << 20)
+    assert _lib.forward_packs_rows(b, s, d, h, f), "shape expected to run on packed rows"
+    cfg = TransformerConfig(b, s, d, h, f, 1, True)
+    model = build_model(cfg, seed=41)
+    x16, _ = make_inputs(cfg, False, 42)
+    g = torch.Generator().manual_seed(43)
+    lengths = torch.randint(0, s + 1, (b,), generator=g)
+    lengths[:3] = torch.tensor([0, s, 7])
+    mask = torch.arange(s)[None, :] < lengths[:, None]
+    x16 = x16.masked_fill(~mask[..., None], 0)
+    gm = copy.deepcopy(model).half().to(device).eval()
+    opt = make_optimized_transformer(copy.deepcopy(gm))
+    xd, md = x16.to(device), mask.to(device)
+    lib = _lib.load()
+    with torch.inference_mode():
+        y = opt(xd, md)
+        _lib.check(lib.tt_forward_packing_override(0), "packing override")
+        try:
+            y_pad = opt(xd, md)
+        finally:
+            lib.tt_forward_packing_override(-1)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_pad)
+    assert bool((y.cpu()[~mask] == 0).all()) and not torch.signbit(y.cpu()[~mask]).any()
+    params = O.params_fp32(gm)
+    for i in (0, 1, 2, 1000, b - 1):
+        ref = O.forward(params, x16[i:i + 1].float(), mask[i:i + 1], h, True)
+        res = O.check_tolerance(y[i:i + 1], ref, mask[i:i + 1])
+        print(f"[packed-long] seq {i} len {int(lengths[i])} {res}", flush=True)
+        assert res["passed"], (i, res)
+
+
 # The reference's input-scale sweep (benchmarks/benchmark_steps_1_2.py:28) on the C1 (layer-wise,
 # LayerNorm folded into the projections), C2 (persistent megakernel) and C3 (masked, packed rows)
 # shapes.
