@@ -223,6 +223,72 @@ def kernel_breakdown(name, dev, iters=20):
     return res
 
 
+def library_gemms(name, dev, iters=20):
+    """Each projection of one layer of ``name`` three ways on the same operands (the forward's LN2
+    output, attention context and GELU activations, the last layer's weights): this build's kernel
+    with the forward's fused epilogue, this build's kernel with a bias-only epilogue, and the
+    vendor library through torch (``F.linear``: hipBLASLt, bias fused), alone and followed by the
+    unfused epilogue ops that would complete it (GELU, residual add).  Average per launch (us)."""
+    import torch.nn.functional as Fn
+    cfg = WORKLOADS[name].config
+    B, S, D, H, F, L = (cfg.batch_size, cfg.seq_len, cfg.d_model, cfg.num_heads, cfg.ffn_dim,
+                        cfg.num_layers)
+    T = B * S
+    x16, mask = workload_inputs(name)
+    model = build_model(cfg).half().to(dev).eval()
+    opt = make_optimized_transformer(copy.deepcopy(model), plan=PLAN_LAYERWISE)
+    xd = x16.to(dev)
+    md = None if mask is None else mask.to(dev)
+    with torch.inference_mode():
+        opt(xd, md)
+    torch.cuda.synchronize()
+    ws = opt.last_workspace
+    _, _, oh = _lib.stage_offsets(B, S, D, H, F, L, PLAN_LAYERWISE)
+    half = lambda off, n: ws[off:off + 2 * n].view(torch.float16)
+    xa = half(0, T * D).view(T, D).clone()
+    xn = half((T * D * 2 + 255) // 256 * 256, T * D).view(T, D).clone()
+    hmid = half(oh, T * F).view(T, F).clone()
+    offs, stride, _, _ = _lib.weight_layout(D, F, L)
+    wl = opt.packed_weights[(L - 1) * stride:]
+    seg = lambda i, n: wl[offs[i]:offs[i] + n]
+    wqkv, bqkv = seg(2, 3 * D * D).view(3 * D, D), seg(3, 3 * D)
+    wo, bo = seg(4, D * D).view(D, D), seg(5, D)
+    w1, b1 = seg(8, F * D).view(F, D), seg(9, F)
+    w2, b2 = seg(10, D * F).view(D, F), seg(11, D)
+    ctx = xn.clone()  # an activation of the context's shape and magnitude
+    resid = xa.clone()
+    gemms = {
+        "qkv": (lambda: ops.qkv_projection(xn.reshape(B, S, D), wqkv, bqkv, H),
+                lambda: ops.linear(xn, wqkv, bqkv, "bias"),
+                lambda: Fn.linear(xn, wqkv, bqkv), None, 2 * T * 3 * D * D),
+        "out_proj": (lambda: ops.linear(ctx, wo, bo, "resid_masked", residual=resid, valid=md,
+                                        out=resid),
+                     lambda: ops.linear(ctx, wo, bo, "bias"),
+                     lambda: Fn.linear(ctx, wo, bo), lambda y: y.add_(xa), 2 * T * D * D),
+        "ffn_in": (lambda: ops.linear(xn, w1, b1, "gelu"), lambda: ops.linear(xn, w1, b1, "bias"),
+                   lambda: Fn.linear(xn, w1, b1), lambda y: Fn.gelu(y), 2 * T * D * F),
+        "ffn_out": (lambda: ops.linear(hmid, w2, b2, "masked_resid", residual=resid, valid=md,
+                                       out=resid),
+                    lambda: ops.linear(hmid, w2, b2, "bias"),
+                    lambda: Fn.linear(hmid, w2, b2), lambda y: y.add_(xa), 2 * T * F * D),
+    }
+    res = {}
+    with torch.inference_mode():
+        for gname, (fused, bias, lib_fn, lib_epi, flops) in gemms.items():
+            runs = {"ours_fused": fused, "ours_bias": bias, "library_bias": lib_fn}
+            if lib_epi is not None:
+                runs["library_plus_epilogue_ops"] = lambda f=lib_fn, g=lib_epi: g(f())
+            entry = {"flops": flops}
+            for tag, fn in runs.items():
+                for _ in range(3):
+                    fn()
+                t = statistics.median(loop_time(fn, iters) for _ in range(3))
+                entry[tag + "_us"] = t * 1e3
+                entry[tag + "_frac"] = flops / (t * 1e-3) / 1e12 / PEAK_TFLOPS
+            res[gname] = entry
+    return res
+
+
 COPY_ELEMS = 64 * 1024 * 1024  # fp16 elements: 128 MiB read + 128 MiB written per copy
 
 
@@ -447,12 +513,14 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-eager", action="store_true")
     ap.add_argument("--mode", default="full",
-                    choices=("full", "kernels", "forward", "trace", "cases"),
+                    choices=("full", "kernels", "forward", "trace", "cases", "library"),
                     help="kernels: only run each kernel of one layer (and a copy of known size) "
                          "a few times, for rocprofv3 counter runs; forward: only run the "
                          "workload's own forward --steps times; trace: per-task summary of the "
                          "megakernel's trace on the workload's shape; cases: time the "
-                         "reference's own 14-case shape table against eager fp16 (one JSON line)")
+                         "reference's own 14-case shape table against eager fp16 (one JSON line); "
+                         "library: each projection of one layer against the vendor library "
+                         "(F.linear, hipBLASLt) on the same operands")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -474,6 +542,9 @@ def main() -> int:
         return 0
     if args.mode == "trace":
         print(json.dumps(megakernel_trace_summary(name, dev)))
+        return 0
+    if args.mode == "library":
+        print(json.dumps({"workload": name, "gemms": library_gemms(name, dev, iters=args.steps)}))
         return 0
     if args.mode == "kernels":
         copy_calibration(dev)
