@@ -544,6 +544,7 @@ def main() -> int:
         print(json.dumps(megakernel_trace_summary(name, dev)))
         return 0
     if args.mode == "library":
+        copy_calibration(dev)
         print(json.dumps({"workload": name, "gemms": library_gemms(name, dev, iters=args.steps)}))
         return 0
     if args.mode == "kernels":
