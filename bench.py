@@ -224,8 +224,9 @@ def kernel_breakdown(name, dev, iters=20):
 
 
 def library_gemms(name, dev, iters=20):
-    """Each projection of one layer of ``name`` three ways on the same operands (the forward's LN2
-    output, attention context and GELU activations, the last layer's weights): this build's kernel
+    """Each projection of one layer of ``name`` three ways on the same operands (the forward's
+    residual stream and GELU activations, their LayerNorm with the last layer's norm2, the last
+    layer's weights): this build's kernel
     with the forward's fused epilogue, this build's kernel with a bias-only epilogue, and the
     vendor library through torch (``F.linear``: hipBLASLt, bias fused), alone and followed by the
     unfused epilogue ops that would complete it (GELU, residual add).  Average per launch (us)."""
@@ -245,12 +246,12 @@ def library_gemms(name, dev, iters=20):
     ws = opt.last_workspace
     _, _, oh = _lib.stage_offsets(B, S, D, H, F, L, PLAN_LAYERWISE)
     half = lambda off, n: ws[off:off + 2 * n].view(torch.float16)
-    xa = half(0, T * D).view(T, D).clone()
-    xn = half((T * D * 2 + 255) // 256 * 256, T * D).view(T, D).clone()
+    xa = half(0, T * D).view(T, D).clone()  # the residual stream leads the workspace
     hmid = half(oh, T * F).view(T, F).clone()
     offs, stride, _, _ = _lib.weight_layout(D, F, L)
     wl = opt.packed_weights[(L - 1) * stride:]
     seg = lambda i, n: wl[offs[i]:offs[i] + n]
+    xn = ops.layernorm(xa, seg(6, D), seg(7, D))  # an LN2 output of the forward's magnitude
     wqkv, bqkv = seg(2, 3 * D * D).view(3 * D, D), seg(3, 3 * D)
     wo, bo = seg(4, D * D).view(D, D), seg(5, D)
     w1, b1 = seg(8, F * D).view(F, D), seg(9, F)
