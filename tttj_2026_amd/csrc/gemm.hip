@@ -275,9 +275,13 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 && BM * BN <= 128 * 128) ? 2 : 1)
 
     // Copies of the next stage per k-step: C0 in the first (they have the whole stage to land),
     // the rest spread evenly over the others, so that no wave issues a burst of copies (each one
-    // holds the wave's issue for ~100 cycles when the CU's copy queue is busy).  An 8-wave block
-    // issues all of them at once: the other wave of the SIMD keeps the MFMAs busy meanwhile.
-    constexpr int C0 = NW == 8 ? NL : (NL + 3) / 4;
+    // holds the wave's issue for ~100 cycles when the CU's copy queue is busy).  The 8-wave
+    // 256 x 256 block (two stages) issues all of them in the first k-step, since they have one
+    // stage to land; with the three-stage ring a copy has two stages, and one copy in the first
+    // k-step, the rest spread (1, 2, 2, 1 for 256 x 128), keeps the two waves of a SIMD from
+    // blocking together (measured on MI355X: C5 out_proj 24.2 -> 23.3, ffn_out 68.9 -> 65.8 us;
+    // spreading the two-stage block's copies slows ffn_in by 6-10%).
+    constexpr int C0 = NW == 8 ? (NS == 3 ? 1 : NL) : (NL + 3) / 4;
     constexpr int CPER = (NL - C0 + KSUB - 2) / (KSUB - 1);
     // One stage: KSUB k-steps of FN x FM MFMAs; the next k-step's fragment reads and this
     // k-step's copies of stage kn are interleaved one per MFMA.
