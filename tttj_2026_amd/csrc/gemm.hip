@@ -960,14 +960,18 @@ static int g_tile_override = -1;  // test hook: force one tile configuration
 // for few-token grids.  Exactly one round of 8-wave 256 x 128 tiles with the three-stage ring
 // (N = 1024 at M = 8192) beats two 128 x 128 blocks per CU inside the forward, with or without a
 // row mask (same-process A/B of whole forwards: C5 -2.5%, C4 with 20% padded rows -3.4%), although
-// a GEMM repeated on its own favours the 128-row tiles for out_proj and for padded rows.
-static int pick_tile(int m, int n, int k, int mode, int cus) {
-  (void)mode;
+// a GEMM repeated on its own favours the 128-row tiles for out_proj and for padded rows.  The QKV
+// projection takes the same tile for whole rounds of it (C5, 8192 x 3072 x 1024: three rounds;
+// forward -2.0%) unless its live row count is read on the device (packed rows, whose live tiles
+// end inside a round: C4 +0.4 / +0.8% with it).
+static int pick_tile(int m, int n, int k, int mode, int cus, bool packed = false) {
   if (g_tile_override >= 0 && g_tile_override < kNumTiles && n % kTiles[g_tile_override].bn == 0)
     return g_tile_override;
   auto tiles = [&](int i) { return (long)((m + kTiles[i].bm - 1) / kTiles[i].bm) * (n / kTiles[i].bn); };
   if (n % 256 == 0 && tiles(0) >= 2 * cus && tiles(0) % cus == 0) return 0;
-  if (n % 128 == 0 && k >= 1024 && tiles(10) == cus) return 10;
+  if (n % 128 == 0 && k >= 1024 &&
+      (tiles(10) == cus || (mode == TT_EPI_QKV && !packed && tiles(10) % cus == 0)))
+    return 10;
   // One round of 128 x 64 tiles streaming a long K is latency-bound: each CU moves only the bytes
   // it keeps in flight, and the register path keeps two more K stages in flight than the direct
   // copies (measured on MI355X, 4096 x 512 x 2048: 22.3 -> 15.8 us).  On grids of several tiles
@@ -1054,7 +1058,7 @@ int launch_linear(const half* x, const half* w, int m, int n, int k, const EpiAr
   }
   if (m == 0) return TT_OK;
   if (k % kBK != 0 || n % 64 != 0) return run_small(ep.mode, x, w, m, n, k, ep, stream);
-  const int tile = pick_tile(m, n, k, ep.mode, device_cus());
+  const int tile = pick_tile(m, n, k, ep.mode, device_cus(), ep.m_dev != nullptr);
   if (tile == 5) return run_narrow(ep.mode, x, w, m, n, k, ep, stream);
   switch (ep.mode) {
     case TT_EPI_BIAS: return run_mode<TT_EPI_BIAS>(tile, x, w, m, n, k, ep, stream);
